@@ -1,0 +1,117 @@
+/*
+ * vk_gemm.h -- C ABI of the MI355X (gfx950) GEMM kernel suite.
+ *
+ * One shared library, libvk_gemm.so, built from vibekernel_amd/csrc/ with
+ * hipcc --offload-arch=gfx950.  Plain C types only: no HIP, torch or C++
+ * types cross this boundary (a stream is passed as void*, NULL = the null
+ * stream of the current device).
+ *
+ * Reference interface replaced (paths relative to the reference repository):
+ *   results/naive_cycle4/include/playground/matmul.hpp:11-13
+ *     template <typename DType, uint8_t Version>
+ *     void matmul(size_t m, size_t n, size_t k, const DType* A, const DType* B, DType* C);
+ *   specialised per version by PLAYGROUND_MATMUL_DEC (matmul.hpp:16-19) and
+ *   called through PLAYGOUND_MATMUL_CALL (matmul.hpp:21-23) from
+ *   results/ralph_loop_fable/src/main.cpp:38-41.
+ *
+ * Semantics kept from the reference:
+ *   C = A . B, all three row-major and dense (lda = k, ldb = n, ldc = n),
+ *   alpha = 1, beta = 0: C is fully overwritten and never read
+ *   (matmul_f16_v0_cblas.cpp:22-23).  A, B, C are DEVICE pointers for every
+ *   version >= 1 (main.cpp:49-51).  The launch is asynchronous on the stream;
+ *   nothing inside synchronises.  fp16 inputs are accumulated in fp32.
+ *
+ * Differences (the reference returns void and has no error channel):
+ *   every entry point returns VK_OK or a negative vk_status and never exits;
+ *   the output dtype may be fp32 as well as the input dtype;
+ *   the stream is explicit; version 0 (the CPU cBLAS ground truth) is not in
+ *   this library -- it lives with the task1 harness, as in the reference.
+ */
+#ifndef VK_GEMM_H
+#define VK_GEMM_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define VK_GEMM_ABI_VERSION 1
+
+typedef enum vk_dtype {
+  VK_DTYPE_F16 = 1, /* IEEE binary16 ("float16_t" = half in the reference, system.hpp:29) */
+  VK_DTYPE_F32 = 2  /* IEEE binary32 ("float32_t", system.hpp:27) */
+} vk_dtype;
+
+typedef enum vk_status {
+  VK_OK = 0,
+  VK_ERR_VERSION = -1,   /* no such version for this input dtype */
+  VK_ERR_DTYPE = -2,     /* unsupported (input, output) dtype pair */
+  VK_ERR_SHAPE = -3,     /* shape not handled by this version (see vk_caps) */
+  VK_ERR_ALIGN = -4,     /* a pointer is not aligned as this version needs */
+  VK_ERR_NULL = -5,      /* NULL operand with a non-empty shape */
+  VK_ERR_WORKSPACE = -6, /* caller workspace smaller than vk_gemm_workspace_bytes() */
+  VK_ERR_HIP = -7,       /* HIP runtime error (launch, allocation, device query) */
+  VK_ERR_RANGE = -8      /* a dimension exceeds what the version indexes (2^31-1) */
+} vk_status;
+
+/* What a version handles.  A shape is accepted when m % div_m == 0,
+ * n % div_n == 0, k % div_k == 0, m <= max_m, and the operands are aligned to
+ * align_bytes.  tolerance_tier: 0 = fp32 accumulation in one pass (the
+ * reference's strict tier, mean relative error ~3e-5 on N(0,1) data);
+ * 1 = relaxed (partials rounded below fp32). */
+typedef struct vk_caps {
+  int version;
+  int in_dtype;
+  int out_dtype_mask; /* bit (1 << vk_dtype) set for each supported output */
+  uint32_t div_m, div_n, div_k;
+  uint64_t max_m;
+  uint32_t align_bytes;
+  uint32_t tile_m, tile_n, tile_k; /* workgroup macro tile */
+  uint32_t threads;                /* threads per workgroup */
+  uint32_t lds_bytes;              /* LDS per workgroup */
+  int tolerance_tier;
+  int uses_workspace;
+} vk_caps;
+
+/* C = A . B on `stream`.  Library-managed workspace: a version that needs one
+ * allocates it on its first call on a device (like the reference's
+ * function-local statics, matmul_f16_v42_shfl2.cu:496-519) and keeps it until
+ * vk_gemm_release() or process exit. */
+int vk_gemm(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, size_t n, size_t k,
+            const void* A, const void* B, void* C, void* stream);
+
+/* Same, with a caller-owned device workspace of at least
+ * vk_gemm_workspace_bytes() bytes (may be NULL when that is 0).  Never
+ * allocates. */
+int vk_gemm_ws(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, size_t n, size_t k,
+               const void* A, const void* B, void* C, void* workspace, size_t workspace_bytes,
+               void* stream);
+
+size_t vk_gemm_workspace_bytes(int version, vk_dtype in_dtype, size_t m, size_t n, size_t k);
+
+/* Short name of a version ("f16_v2_dma256", ...), or NULL if unknown. */
+const char* vk_gemm_name(int version, vk_dtype in_dtype);
+
+/* Fill *caps; VK_ERR_VERSION if unknown. */
+int vk_gemm_query(int version, vk_dtype in_dtype, vk_caps* caps);
+
+/* Write up to max_count version ids for in_dtype into out; return how many
+ * exist. */
+int vk_gemm_list(vk_dtype in_dtype, int* out, int max_count);
+
+/* Check a call without launching: the same validation vk_gemm performs. */
+int vk_gemm_check(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, size_t n, size_t k,
+                  const void* A, const void* B, const void* C);
+
+/* Free library-managed workspaces on every device. */
+int vk_gemm_release(void);
+
+const char* vk_status_string(int status);
+int vk_gemm_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* VK_GEMM_H */

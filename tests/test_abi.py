@@ -1,0 +1,97 @@
+"""C ABI of libvk_gemm.so, checked without a GPU: the library loads, exports
+every entry point include/vk_gemm.h declares, and validates arguments the way
+the header documents (no kernel is launched by any of these calls)."""
+import ctypes
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def _header_functions():
+    text = open(os.path.join(ROOT, "include", "vk_gemm.h")).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(vk_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_library_exports_every_header_symbol():
+    from vibekernel_amd import _abi
+    L = _abi.load()
+    declared = _header_functions()
+    assert declared, "no declarations parsed"
+    for fn in declared:
+        assert hasattr(L, fn), f"{fn} declared in include/vk_gemm.h but not exported"
+    assert sorted(_abi.EXPORTED_SYMBOLS) == declared
+
+
+def test_abi_version_and_registry():
+    from vibekernel_amd import _abi
+    assert _abi.abi_version() == 1
+    f16 = _abi.versions(_abi.DTYPE_F16)
+    f32 = _abi.versions(_abi.DTYPE_F32)
+    assert 1 in f16 and 2 in f16 and 1 in f32
+    assert 0 not in f16  # v0 (CPU ground truth) lives with the harness, not here
+    for v in f16:
+        assert _abi.name(v, _abi.DTYPE_F16).startswith(f"f16_v{v}_")
+    assert _abi.name(99, _abi.DTYPE_F16) is None
+
+
+F16, F32 = 1, 2
+P = 1 << 20  # a 16-byte-aligned fake address: vk_gemm_check never dereferences
+
+
+@pytest.mark.parametrize("args,expected", [
+    ((2, F16, F16, 4096, 4096, 4096, P, P, P), 0),
+    ((2, F16, F32, 4096, 4096, 4096, P, P, P), 0),
+    ((2, F16, F16, 4096, 4096, 4000, P, P, P), -3),    # k % 64
+    ((2, F16, F16, 4000, 4096, 4096, P, P, P), -3),    # m % 256
+    ((2, F16, F16, 4096, 4096, 4096, P + 2, P, P), -4),  # A misaligned
+    ((2, F16, F16, 4096, 4096, 4096, 0, P, P), -5),    # NULL A
+    ((2, F16, F16, 0, 4096, 4096, 0, 0, 0), 0),        # empty: nothing to write
+    ((2, F16, F16, 256, 256, 0, 0, 0, P), 0),          # k == 0: C := 0, A/B unused
+    ((2, F16, F16, 256, 256, 0, 0, 0, 0), -5),         # k == 0 still needs C
+    ((42, F16, F16, 256, 256, 256, P, P, P), -1),      # unknown version
+    ((1, F32, F16, 256, 256, 256, P, P, P), -2),       # f32 in, f16 out unsupported
+    ((1, F16, 7, 256, 256, 256, P, P, P), -2),         # bad dtype code
+    ((1, F16, F16, 17, 33, 65, P + 2, P + 4, P + 6), 0),  # v1: any shape, 2-byte aligned
+    ((1, F16, F16, 2 ** 31, 1, 1, P, P, P), -8),       # beyond 32-bit indexing
+])
+def test_vk_gemm_check(args, expected):
+    from vibekernel_amd import _abi
+    assert _abi.check(*args) == expected
+
+
+def test_status_strings():
+    from vibekernel_amd import _abi
+    for code in range(-8, 1):
+        s = _abi.status_string(code)
+        assert s and s != "unknown status"
+    assert _abi.status_string(-99) == "unknown status"
+
+
+def test_caps_consistent():
+    from vibekernel_amd import _abi
+    for v in _abi.versions(_abi.DTYPE_F16):
+        c = _abi.query(v, _abi.DTYPE_F16)
+        assert c.version == v and c.lds_bytes <= 160 * 1024 and c.threads % 64 == 0
+        assert _abi.DTYPE_F16 in c.out_dtypes
+    with pytest.raises(_abi.VkError):
+        _abi.query(123, _abi.DTYPE_F16)
+
+
+def test_workspace_bytes_zero_for_plain_versions():
+    from vibekernel_amd import _abi
+    for v in _abi.versions(_abi.DTYPE_F16):
+        c = _abi.query(v, _abi.DTYPE_F16)
+        if not c.uses_workspace:
+            assert _abi.workspace_bytes(v, _abi.DTYPE_F16, 4096, 4096, 4096) == 0
+
+
+def test_single_hip_runtime_in_process():
+    """The library must bind to the HIP runtime the process already uses
+    (PyTorch's), never map a second one."""
+    from vibekernel_amd import _abi
+    _abi.load()
+    assert len(_abi.hip_runtimes_loaded()) == 1, _abi.hip_runtimes_loaded()

@@ -1,0 +1,72 @@
+// vk_device.hpp -- gfx950 device helpers shared by the GEMM kernels.
+//
+// Operand layouts of the CDNA4 MFMAs used here (lane l of a 64-wide wave;
+// measured on MI355X with an in-bounds probe before any kernel used them):
+//
+//   v_mfma_f32_32x32x16_f16  D(32x32) += A(32x16) . B(16x32)
+//     A: lane l holds A[l % 32][8 * (l / 32) + e], e = 0..7 (8 halves)
+//     B: lane l holds B[8 * (l / 32) + e][l % 32]
+//     D: lane l, register r holds D[8 * (r / 4) + 4 * (l / 32) + r % 4][l % 32]
+//
+//   v_mfma_f32_16x16x32_f16  D(16x16) += A(16x32) . B(32x16)
+//     A: lane l holds A[l % 16][8 * (l / 16) + e]
+//     B: lane l holds B[8 * (l / 16) + e][l % 16]
+//     D: lane l, register r holds D[4 * (l / 16) + r][l % 16]
+//
+//   ds_read_b64_tr_b16 (LDS transpose read): each lane names 8 bytes (4
+//   halves); inside every group of 16 lanes, lane i receives half (i % 4) of
+//   the 8 bytes named by lane 4 * j + i / 4, for j = 0..3.  Read as a matrix:
+//   the 16 lanes' 64 halves form 4 rows of 16 (row j = lanes 4j..4j+3) and
+//   lane i receives column i.
+//
+//   global_load_lds_dwordx4 (direct-to-LDS): lane l's 16 bytes land at
+//   LDS base + 16 * l; the base comes from M0 and is uniform per wave.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+
+namespace vk {
+
+typedef _Float16 half_t;
+typedef _Float16 half8 __attribute__((ext_vector_type(8)));
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+typedef short short4v __attribute__((ext_vector_type(4)));
+typedef float float16v __attribute__((ext_vector_type(16)));
+typedef float float4v __attribute__((ext_vector_type(4)));
+typedef uint32_t uint4v __attribute__((ext_vector_type(4)));
+
+#define VK_LDS_PTR(T, p) ((__attribute__((address_space(3))) T*)(p))
+
+__device__ __forceinline__ float16v mfma32x32x16(const half8& a, const half8& b, const float16v& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float4v mfma16x16x32(const half8& a, const half8& b, const float4v& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, c, 0, 0, 0);
+}
+
+// 4 halves, transposed across each 16-lane group (see header comment).
+__device__ __forceinline__ half4 lds_read_tr16(const half_t* lds_addr) {
+  short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(VK_LDS_PTR(short4v, lds_addr));
+  return __builtin_bit_cast(half4, r);
+}
+
+// 16 bytes from global straight into LDS at lds_wave_base + 16 * lane.
+__device__ __forceinline__ void global_load_lds16(const void* gptr, void* lds_wave_base) {
+  __builtin_amdgcn_global_load_lds(gptr, VK_LDS_PTR(void, lds_wave_base), 16, 0, 0);
+}
+
+template <typename OutT>
+__device__ __forceinline__ OutT convert_out(float v);
+template <>
+__device__ __forceinline__ half_t convert_out<half_t>(float v) {
+  return (half_t)v;  // v_cvt_f16_f32: round to nearest even (default mode)
+}
+template <>
+__device__ __forceinline__ float convert_out<float>(float v) {
+  return v;
+}
+
+}  // namespace vk

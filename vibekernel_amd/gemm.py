@@ -1,0 +1,93 @@
+"""Python mirror of the reference operator interface.
+
+Reference (paths relative to the reference repository root):
+``results/naive_cycle4/include/playground/matmul.hpp:11-23``::
+
+    template <typename DType, uint8_t Version>
+    void matmul(size_t m, size_t n, size_t k, const DType* A, const DType* B, DType* C);
+    #define PLAYGOUND_MATMUL_CALL(Version, m, n, k, A, B, C) \
+        matmul<remove_cvref_t<decltype(*A)>, Version>(m, n, k, A, B, C)
+
+:func:`matmul` keeps the argument order and meaning: ``m, n, k`` then row-major
+``A`` (m x k), ``B`` (k x n) and the output ``C`` (m x n), which is fully
+overwritten (alpha = 1, beta = 0).  As in ``PLAYGOUND_MATMUL_CALL`` the input
+dtype comes from ``A``; the output dtype comes from ``C`` (fp16 as in the
+reference, or fp32).  Operands are device tensors; the call is asynchronous on
+the current stream (or ``stream``).  Where the reference returns void with no
+error channel, this raises :class:`VkError`.
+
+Every call goes through libvk_gemm.so; there is no other implementation.
+"""
+from __future__ import annotations
+
+from . import _abi
+from ._abi import DTYPE_F16, DTYPE_F32, VkError
+
+
+def _torch():
+    import torch  # imported lazily: the ABI layer itself does not need torch
+    return torch
+
+
+def _dtype_code(t) -> int:
+    torch = _torch()
+    if t.dtype == torch.float16:
+        return DTYPE_F16
+    if t.dtype == torch.float32:
+        return DTYPE_F32
+    raise VkError(-2, f"unsupported dtype {t.dtype}")
+
+
+def _stream_handle(stream, device):
+    torch = _torch()
+    if stream is None:
+        stream = torch.cuda.current_stream(device)
+    return ctypes_void_p(stream.cuda_stream)
+
+
+def ctypes_void_p(v):
+    import ctypes
+    return ctypes.c_void_p(v)
+
+
+def matmul(m: int, n: int, k: int, A, B, C, version: int, stream=None) -> None:
+    """C = A . B with kernel ``version`` (row-major, fp32 accumulation)."""
+    for name, t in (("A", A), ("B", B), ("C", C)):
+        if not t.is_cuda:
+            raise VkError(-5, f"{name} must be a device tensor")
+        if not t.is_contiguous():
+            raise VkError(-4, f"{name} must be contiguous (row-major, dense)")
+    if A.numel() < m * k or B.numel() < k * n or C.numel() < m * n:
+        raise VkError(-3, "operand smaller than m x k / k x n / m x n")
+    in_dt = _dtype_code(A)
+    if _dtype_code(B) != in_dt:
+        raise VkError(-2, "A and B must have the same dtype")
+    out_dt = _dtype_code(C)
+    st = _abi.gemm(version, in_dt, out_dt, m, n, k, A.data_ptr(), B.data_ptr(), C.data_ptr(),
+                   _stream_handle(stream, C.device))
+    if st != _abi.VK_OK:
+        raise VkError(st, f"matmul(version={version}, m={m}, n={n}, k={k})")
+
+
+def gemm(A, B, version: int, out_dtype=None, stream=None):
+    """Allocate C and run :func:`matmul`; A is (m, k), B is (k, n)."""
+    torch = _torch()
+    m, k = A.shape
+    k2, n = B.shape
+    if k != k2:
+        raise VkError(-3, f"inner dimensions differ: {k} vs {k2}")
+    C = torch.empty((m, n), dtype=out_dtype or A.dtype, device=A.device)
+    matmul(m, n, k, A, B, C, version, stream)
+    return C
+
+
+def versions(dtype: str = "f16") -> list:
+    return _abi.versions(DTYPE_F16 if dtype == "f16" else DTYPE_F32)
+
+
+def name(version: int, dtype: str = "f16"):
+    return _abi.name(version, DTYPE_F16 if dtype == "f16" else DTYPE_F32)
+
+
+def query(version: int, dtype: str = "f16"):
+    return _abi.query(version, DTYPE_F16 if dtype == "f16" else DTYPE_F32)
