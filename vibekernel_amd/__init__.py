@@ -7,5 +7,6 @@ and the benchmark.
 from ._abi import DTYPE_F16, DTYPE_F32, VkError, abi_version, lib_path, load  # noqa: F401
 from .gemm import gemm, matmul, name, query, versions  # noqa: F401
 
-# Default fp16 version: the fastest kernel that handles the shape.
-DEFAULT_F16_VERSION = 2
+# Default fp16 version: the fastest kernel for tile-divisible shapes (256x256 tiles,
+# BK=32, 4-stage direct-to-LDS ring).
+DEFAULT_F16_VERSION = 3

@@ -24,6 +24,7 @@
 #include "vk_device.hpp"
 #include "vk_internal.hpp"
 
+#include <atomic>
 #include <type_traits>
 
 namespace vk {
@@ -90,6 +91,16 @@ __device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t
 }
 #pragma clang diagnostic pop
 
+// 4 consecutive outputs, one vector store (8 B for fp16, 16 B for fp32).
+__device__ __forceinline__ void store4(half_t* p, float a, float b, float c, float d) {
+  half4 h = {(half_t)a, (half_t)b, (half_t)c, (half_t)d};
+  *reinterpret_cast<half4*>(p) = h;
+}
+__device__ __forceinline__ void store4(float* p, float a, float b, float c, float d) {
+  float4v f = {a, b, c, d};
+  *reinterpret_cast<float4v*>(p) = f;
+}
+
 template <int BK, int NSTAGE>
 struct Cfg {
   static constexpr int kAChunksPerRow = BK / 8;
@@ -103,6 +114,7 @@ struct Cfg {
   static constexpr int kDmaPerStage = kADma + kBDma;
   static constexpr int kKSteps = BK / 16;
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+  static_assert(kLdsBytes >= 4 * 128 * 128 * 2, "epilogue staging needs 128 KB");
 };
 
 // Tile order: XCD-aware remap plus a grouped raster of GM tile-rows.
@@ -118,6 +130,79 @@ __device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& 
   const int r = cid - g * group;
   tm = first_m + r % gm;
   tn = r / gm;
+}
+
+// LDS bytes each wave uses to stage its 128x128 output block (fp16: the whole
+// block; fp32: half of it per pass).
+constexpr int kEpiWaveBytes = 128 * 128 * 2;
+
+__device__ __forceinline__ void lds_write8(uint32_t addr, half4 v) {
+  *reinterpret_cast<__attribute__((address_space(3))) half4*>(addr) = v;
+}
+__device__ __forceinline__ void lds_write16(uint32_t addr, float4v v) {
+  *reinterpret_cast<__attribute__((address_space(3))) float4v*>(addr) = v;
+}
+__device__ __forceinline__ uint4v lds_read16(uint32_t addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) uint4v*>(addr);
+}
+
+// fp16 output: the wave's 128x128 block, row pitch 256 B = 16 chunks of 16 B,
+// physical chunk = chunk ^ (row % 16).  Read back 4 rows per instruction.
+template <typename OutT>
+__device__ __forceinline__ typename std::enable_if<std::is_same<OutT, half_t>::value>::type
+epilogue_store(float16v (&acc)[4][4], char*, uint32_t wbase, OutT* Cw, int N, int lane) {
+  const int r0 = lane & 31, hsel = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; g4++) {
+        const int row = i * 32 + r0;
+        const int chunk = 4 * j + g4;
+        half4 h = {(half_t)acc[i][j][4 * g4 + 0], (half_t)acc[i][j][4 * g4 + 1],
+                   (half_t)acc[i][j][4 * g4 + 2], (half_t)acc[i][j][4 * g4 + 3]};
+        lds_write8(wbase + row * 256 + 16 * (chunk ^ (row & 15)) + 8 * hsel, h);
+      }
+  const int rsub = lane >> 4, ch = lane & 15;
+#pragma unroll
+  for (int q = 0; q < 32; q++) {
+    const int row = 4 * q + rsub;
+    const uint4v v = lds_read16(wbase + row * 256 + 16 * (ch ^ (row & 15)));
+    *reinterpret_cast<uint4v*>(Cw + (size_t)row * N + ch * 8) = v;
+  }
+}
+
+// fp32 output: two passes of 64 rows (32 KB per wave each), row pitch 512 B =
+// 32 chunks, physical chunk = chunk ^ (row % 32); 2 rows per read.
+template <typename OutT>
+__device__ __forceinline__ typename std::enable_if<std::is_same<OutT, float>::value>::type
+epilogue_store(float16v (&acc)[4][4], char*, uint32_t wbase, OutT* Cw, int N, int lane) {
+  const int r0 = lane & 31, hsel = lane >> 5;
+#pragma unroll
+  for (int pass = 0; pass < 2; pass++) {
+#pragma unroll
+    for (int ii = 0; ii < 2; ii++)
+#pragma unroll
+      for (int j = 0; j < 4; j++)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+          const int i = 2 * pass + ii;
+          const int row = ii * 32 + r0;  // row within this pass
+          const int chunk = 8 * j + 2 * g4 + hsel;
+          float4v f = {acc[i][j][4 * g4 + 0], acc[i][j][4 * g4 + 1], acc[i][j][4 * g4 + 2],
+                       acc[i][j][4 * g4 + 3]};
+          lds_write16(wbase + row * 512 + 16 * (chunk ^ (row & 31)), f);
+        }
+    const int rsub = lane >> 5, ch = lane & 31;
+#pragma unroll
+    for (int q = 0; q < 32; q++) {
+      const int row = 2 * q + rsub;
+      const uint4v v = lds_read16(wbase + row * 512 + 16 * (ch ^ (row & 31)));
+      *reinterpret_cast<uint4v*>(Cw + (size_t)(pass * 64 + row) * N + ch * 4) = v;
+    }
+    if (pass == 0) __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): region reused next pass
+  }
 }
 
 template <int BK, int NSTAGE, typename OutT>
@@ -238,7 +323,7 @@ __global__ __launch_bounds__(kThreads, 1) void f16_dma_kernel(const half_t* __re
 #pragma unroll
     for (int t = 0; t < 16; t++) {
       const int i = t >> 2, j = t & 3;
-      acc[i][j] = mfma32x32x16(fa[cur][i], fb[cur][j], acc[i][j]);
+      acc[i][j] = mfma32x32x16(fb[cur][j], fa[cur][i], acc[i][j]);  // C^T block, see epilogue
       if constexpr (decltype(kReads)::value) {
         if (t < 12) read_slot(t, next_off, next_ks, fa[nxt], fb[nxt]);
       }
@@ -285,41 +370,50 @@ __global__ __launch_bounds__(kThreads, 1) void f16_dma_kernel(const half_t* __re
   // workgroup can exit and its LDS be handed to another workgroup.
   wait_vmcnt<0>();
 
-  // ---- epilogue: D[8*(r/4) + 4*(lane/32) + r%4][lane%32] of each 32x32 block ----
-  OutT* Cw = C + (size_t)(m0 + wm * 128) * N + n0 + wn * 128 + (lane & 31);
-#pragma unroll
-  for (int i = 0; i < 4; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-#pragma unroll
-      for (int r = 0; r < 16; r++) {
-        const int row = i * 32 + 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
-        Cw[(size_t)row * N + j * 32] = convert_out<OutT>(acc[i][j][r]);
-      }
+  // ---- epilogue: C tile staged through LDS, written as full 128-byte lines ----
+  // The MFMAs computed C^T blocks (B fragment as the A operand): lane l,
+  // register r of block (i, j) holds C[i*32 + l%32][j*32 + 8*(r/4) + 4*(l/32)
+  // + r%4], i.e. 4 consecutive columns of one row per register group.  Each
+  // wave writes those 4-value pieces into its own LDS region (the k-loop
+  // stages are free once every wave has passed the barrier below), then reads
+  // the region back row-contiguously so every global store instruction covers
+  // whole 128-byte lines.  The 16-byte chunk index is XORed with the row
+  // (mod 16 / mod 32) to spread the column-wise writes over the banks.
+  lds_barrier();
+  epilogue_store<OutT>(acc, lds + wave * kEpiWaveBytes, lds_addr32(lds) + wave * kEpiWaveBytes,
+                       C + (size_t)(m0 + wm * 128) * N + n0 + wn * 128, N, lane);
+}
+
+// hipFuncSetAttribute(MaxDynamicSharedMemorySize) once per kernel instance
+// and device (a bit per device id).
+template <typename KFn>
+hipError_t ensure_lds_attr(KFn kfn, int bytes, int device, std::atomic<uint64_t>& done) {
+  const uint64_t bit = device < 64 ? (1ull << device) : 0;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kfn),
+                                     hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_acq_rel);
+  return e;
+}
+
+template <int BK, int NSTAGE, typename OutT>
+hipError_t launch_dma_t(const GemmArgs& a) {
+  using G = Cfg<BK, NSTAGE>;
+  static std::atomic<uint64_t> attr_done{0};
+  auto kfn = f16_dma_kernel<BK, NSTAGE, OutT>;
+  hipError_t e = ensure_lds_attr(kfn, G::kLdsBytes, a.device, attr_done);
+  if (e != hipSuccess) return e;
+  const int tiles = (int)((a.m / kBM) * (a.n / kBN));
+  hipLaunchKernelGGL(kfn, dim3(tiles), dim3(kThreads), G::kLdsBytes, a.stream,
+                     static_cast<const half_t*>(a.A), static_cast<const half_t*>(a.B),
+                     static_cast<OutT*>(a.C), (int)a.m, (int)a.n, (int)a.k);
+  return hipGetLastError();
 }
 
 template <int BK, int NSTAGE>
 hipError_t launch_dma(const GemmArgs& a) {
-  using G = Cfg<BK, NSTAGE>;
-  const int tiles = (int)((a.m / kBM) * (a.n / kBN));
-  const half_t* A = static_cast<const half_t*>(a.A);
-  const half_t* B = static_cast<const half_t*>(a.B);
-  if (a.out_dtype == VK_DTYPE_F16) {
-    auto kfn = f16_dma_kernel<BK, NSTAGE, half_t>;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kfn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, G::kLdsBytes);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kfn, dim3(tiles), dim3(kThreads), G::kLdsBytes, a.stream, A, B,
-                       static_cast<half_t*>(a.C), (int)a.m, (int)a.n, (int)a.k);
-  } else {
-    auto kfn = f16_dma_kernel<BK, NSTAGE, float>;
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kfn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, G::kLdsBytes);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL(kfn, dim3(tiles), dim3(kThreads), G::kLdsBytes, a.stream, A, B,
-                       static_cast<float*>(a.C), (int)a.m, (int)a.n, (int)a.k);
-  }
-  return hipGetLastError();
+  return a.out_dtype == VK_DTYPE_F16 ? launch_dma_t<BK, NSTAGE, half_t>(a)
+                                     : launch_dma_t<BK, NSTAGE, float>(a);
 }
 
 // 32-bit byte offsets inside one 256-row panel of A and one BK-row slab of B
