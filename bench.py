@@ -20,6 +20,7 @@ Prints ONE JSON line.  Extra objects:
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import sys
@@ -70,6 +71,22 @@ def read_traffic(kernel_name: str, workload: str):
             except (KeyError, ValueError):
                 return None
     return None
+
+
+def load_bench_lib():
+    """libvk_bench.so: the harness timing loops (include/vk_bench.h)."""
+    path = os.path.join(ROOT, "vibekernel_amd", "lib", "libvk_bench.so")
+    if not os.path.exists(path):
+        raise RuntimeError(f"{path} is missing: run __graft_entry__.build()")
+    L = ctypes.CDLL(path)
+    ci, sz, vp = ctypes.c_int, ctypes.c_size_t, ctypes.c_void_p
+    L.vkb_reference_loop.argtypes = [ci, ci, ci, sz, sz, sz, vp, vp, vp, vp, ci, ci,
+                                     ctypes.POINTER(ctypes.c_float)]
+    L.vkb_reference_loop.restype = ci
+    L.vkb_back_to_back.argtypes = [ci, ci, ci, sz, sz, sz, vp, vp, vp, vp, ci,
+                                   ctypes.POINTER(ctypes.c_float)]
+    L.vkb_back_to_back.restype = ci
+    return L
 
 
 def cpu_baseline(m, n, k, dtype, seed, budget_s):
@@ -140,40 +157,38 @@ def main():
     C = torch.empty((m, n), dtype=odt, device=dev)
     stream = torch.cuda.current_stream(dev)
 
-    def step():
-        vk.matmul(m, n, k, A, B, C, version, stream)
+    bench = load_bench_lib()
+    in_code = vk.DTYPE_F16 if dtype == "f16" else vk.DTYPE_F32
+    out_code = vk.DTYPE_F16 if out == "f16" else vk.DTYPE_F32
+    sptr = ctypes.c_void_p(stream.cuda_stream)
+    call = (version, in_code, out_code, m, n, k, ctypes.c_void_p(A.data_ptr()),
+            ctypes.c_void_p(B.data_ptr()), ctypes.c_void_p(C.data_ptr()), sptr)
 
-    for _ in range(args.warmup):
-        step()
-    torch.cuda.synchronize()
-
-    # Timed region: the reference loop (event pair + host sync per launch).
-    starts = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
-    stops = [torch.cuda.Event(enable_timing=True) for _ in range(args.steps)]
+    # Timed region: the reference loop (main.cpp:52-62) run in C++ on the
+    # kernel's stream: warm-up calls, then each call between its own event
+    # pair with a host sync.  Bracketed by device synchronisations.
+    per = (ctypes.c_float * args.steps)()
     torch.cuda.synchronize()
     w0 = time.perf_counter()
-    for i in range(args.steps):
-        starts[i].record(stream)
-        step()
-        stops[i].record(stream)
-        stops[i].synchronize()
+    st = bench.vkb_reference_loop(*call, args.warmup, args.steps, per)
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
-    per_ms = [s.elapsed_time(e) for s, e in zip(starts, stops)]
+    if st != 0:
+        print(f"bench.py: reference loop failed with status {st}", file=sys.stderr)
+        return 1
+    per_ms = list(per)
     mean_ms = sum(per_ms) / len(per_ms)
     flop = 2.0 * m * n * k
     tflops = flop / (mean_ms * 1e-3) / 1e12
 
     # Diagnostic after the timed region: back-to-back launches between one
     # event pair (no host sync in between).
-    e0 = torch.cuda.Event(enable_timing=True)
-    e1 = torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for _ in range(args.steps):
-        step()
-    e1.record(stream)
-    e1.synchronize()
-    b2b_ms = e0.elapsed_time(e1) / args.steps
+    tot = ctypes.c_float(0.0)
+    st = bench.vkb_back_to_back(*call, args.steps, ctypes.byref(tot))
+    if st != 0:
+        print(f"bench.py: back-to-back loop failed with status {st}", file=sys.stderr)
+        return 1
+    b2b_ms = tot.value / args.steps
 
     # Sanity of the timed output against torch's own GEMM (fp32 accumulate);
     # the parity tests hold the real oracle comparison.

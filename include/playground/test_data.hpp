@@ -1,0 +1,165 @@
+// playground/test_data.hpp -- host/device operands, ground truth and the error
+// statistic of the task1 harness.
+// Reference: results/naive_cycle4/include/playground/test_data.hpp:16-210.
+//
+// Kept: CudaDeviceMemPtr-style RAII over device memory (here hipMalloc),
+// host vectors A, B, C, GT; GT computed by version 0 in the constructor; H2D
+// copies of A and B; D2H copy of C; C on the device is never initialised (a
+// kernel must overwrite it); the statistic mean(|GT - C| / |GT|) accumulated
+// sequentially in fp32 with an abort on inf/nan (test_data.hpp:145-162).
+// Changed: inputs come from a seeded generator (the reference seeds from
+// std::random_device and cannot be reproduced) with a choice of
+// distribution; GT == 0 terms are skipped by default (the reference's later
+// base does this; `legacy` mode keeps the original abort); a non-finite C
+// element always aborts; device allocations and copies are checked.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cmath>
+#include <cstdint>
+#include <random>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+#include "playground/matmul.hpp"
+#include "playground/system.hpp"
+#include "playground/utils.hpp"
+
+namespace playground {
+
+template <typename DType>
+class HipDeviceMemPtr {
+public:
+    HipDeviceMemPtr() = default;
+    explicit HipDeviceMemPtr(size_t count) {
+        if (count) PLAYGROUND_HIP_CHECK(hipMalloc(reinterpret_cast<void**>(&ptr_), count * sizeof(DType)));
+    }
+    HipDeviceMemPtr(const HipDeviceMemPtr&) = delete;
+    auto operator=(const HipDeviceMemPtr&) -> HipDeviceMemPtr& = delete;
+    HipDeviceMemPtr(HipDeviceMemPtr&& o) noexcept : ptr_(o.ptr_) { o.ptr_ = nullptr; }
+    auto operator=(HipDeviceMemPtr&& o) noexcept -> HipDeviceMemPtr& {
+        if (this != &o) {
+            if (ptr_) (void)hipFree(ptr_);
+            ptr_ = o.ptr_;
+            o.ptr_ = nullptr;
+        }
+        return *this;
+    }
+    ~HipDeviceMemPtr() {
+        if (ptr_) (void)hipFree(ptr_);
+    }
+    [[nodiscard]] auto get_mutable_raw_ptr() -> DType* { return ptr_; }
+    [[nodiscard]] auto get_const_raw_ptr() const -> const DType* { return ptr_; }
+
+private:
+    DType* ptr_ = nullptr;
+};
+
+enum class Dist { Normal, Uniform, Normal05 };
+
+struct TestConfig {
+    Dist dist = Dist::Normal;     // the reference draws N(0,1)
+    uint64_t seed = 20261201;
+    bool legacy_err = false;      // abort on GT == 0 like the original statistic
+};
+
+inline Dist parse_dist(const std::string& s) {
+    if (s == "normal") return Dist::Normal;
+    if (s == "uniform") return Dist::Uniform;
+    if (s == "normal0.5") return Dist::Normal05;
+    throw std::invalid_argument("unknown distribution '" + s + "' (normal|uniform|normal0.5)");
+}
+
+class TestData {
+public:
+    TestData(uint32_t m, uint32_t n, uint32_t k, TestConfig cfg = {}) : _m(m), _n(n), _k(k), _cfg(cfg) {
+        initHostData();
+        calculateGroundTruth();
+    }
+
+    [[nodiscard]] auto get_mutable_A_ptr() -> params::DataType* { return _A.data(); }
+    [[nodiscard]] auto get_mutable_B_ptr() -> params::DataType* { return _B.data(); }
+    [[nodiscard]] auto get_mutable_C_ptr() -> params::DataType* { return _C.data(); }
+    [[nodiscard]] auto get_mutable_GT_ptr() -> params::DataType* { return _GT.data(); }
+    [[nodiscard]] auto get_mutable_d_A_ptr() -> params::DataType* { return _d_A.get_mutable_raw_ptr(); }
+    [[nodiscard]] auto get_mutable_d_B_ptr() -> params::DataType* { return _d_B.get_mutable_raw_ptr(); }
+    [[nodiscard]] auto get_mutable_d_C_ptr() -> params::DataType* { return _d_C.get_mutable_raw_ptr(); }
+
+    void initHostData() {
+        _A.resize(size_t(_m) * _k);
+        _B.resize(size_t(_k) * _n);
+        _C.resize(size_t(_m) * _n);
+        _GT.resize(size_t(_m) * _n);
+        std::mt19937_64 gen(_cfg.seed);
+        auto fill = [&](std::vector<params::DataType>& v) {
+            if (_cfg.dist == Dist::Uniform) {
+                std::uniform_real_distribution<float64_t> d(-1.0, 1.0);
+                for (auto& x : v) x = params::DataType(d(gen));
+            } else {
+                std::normal_distribution<float64_t> d(0.0, _cfg.dist == Dist::Normal ? 1.0 : 0.5);
+                for (auto& x : v) x = params::DataType(d(gen));
+            }
+        };
+        fill(_A);
+        fill(_B);
+    }
+
+    // Mean relative error, test_data.hpp:145-162, plus the skip-zero rule.
+    [[nodiscard]] auto calculateAvgErr() -> float32_t {
+        float32_t errSum = 0.0F;
+        size_t valid = 0;
+        for (size_t i = 0; i < _GT.size(); ++i) {
+            const float32_t g = float32_t(_GT[i]);
+            const float32_t c = float32_t(_C[i]);
+            PLAYGROUND_CHECK(!std::isnan(c));
+            PLAYGROUND_CHECK(!std::isinf(c));
+            if (!_cfg.legacy_err && g == 0.0F) continue;
+            const float32_t gap = g - c;
+            errSum += std::abs(gap / g);
+            ++valid;
+            PLAYGROUND_CHECK(!std::isinf(errSum));
+            PLAYGROUND_CHECK(!std::isnan(errSum));
+        }
+        PLAYGROUND_CHECK(valid > 0 || _GT.empty());
+        return valid ? errSum / float32_t(valid) : 0.0F;
+    }
+
+    void calculateGroundTruth() {
+        if constexpr (std::is_same_v<params::DataType, float32_t>) {
+            PLAYGOUND_MATMUL_CALL(PG_MATMUL_FP32_CBLAS, _m, _n, _k, _A.data(), _B.data(), _GT.data());
+        } else if constexpr (std::is_same_v<params::DataType, float16_t>) {
+            PLAYGOUND_MATMUL_CALL(PG_MATMUL_FP16_CBLAS, _m, _n, _k, _A.data(), _B.data(), _GT.data());
+        } else {
+            throw std::runtime_error("Unsupported data type");
+        }
+    }
+
+    void initDeviceData() {
+        _d_A = HipDeviceMemPtr<params::DataType>(_A.size());
+        _d_B = HipDeviceMemPtr<params::DataType>(_B.size());
+        _d_C = HipDeviceMemPtr<params::DataType>(_C.size());
+        if (!_A.empty())
+            PLAYGROUND_HIP_CHECK(hipMemcpy(_d_A.get_mutable_raw_ptr(), _A.data(),
+                                           _A.size() * sizeof(params::DataType), hipMemcpyHostToDevice));
+        if (!_B.empty())
+            PLAYGROUND_HIP_CHECK(hipMemcpy(_d_B.get_mutable_raw_ptr(), _B.data(),
+                                           _B.size() * sizeof(params::DataType), hipMemcpyHostToDevice));
+    }
+
+    void copyResultD2H() {
+        if (!_C.empty())
+            PLAYGROUND_HIP_CHECK(hipMemcpy(_C.data(), _d_C.get_mutable_raw_ptr(),
+                                           _C.size() * sizeof(params::DataType), hipMemcpyDeviceToHost));
+    }
+
+private:
+    uint32_t _m, _n, _k;
+    TestConfig _cfg;
+    std::vector<params::DataType> _A, _B, _C, _GT;
+    HipDeviceMemPtr<params::DataType> _d_A, _d_B, _d_C;
+};
+
+}  // namespace playground

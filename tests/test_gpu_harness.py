@@ -1,0 +1,61 @@
+"""The task1 binaries for GPU versions, end to end on the GPU: reference
+result line, error statistic against the binary's own v0 ground truth, and
+the C++ timing loops behind bench.py (include/vk_bench.h)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from gpu_util import announce
+
+pytestmark = pytest.mark.gpu
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+BIN = os.path.join(ROOT, "vibekernel_amd", "harness", "bin")
+RESULT_RE = re.compile(r"TFLOPS: (?P<tf>[0-9.eE+-]+); *Average Error: (?P<err>[0-9.eE+-]+)")
+
+
+@pytest.mark.parametrize("binary,shape,bound", [
+    ("task1_float16_v1", (512, 512, 512), 2e-4),
+    ("task1_float16_v2", (1024, 512, 256), 2e-4),
+    ("task1_float16_v3", (1024, 1024, 1024), 2e-4),
+    ("task1_float32_v1", (512, 384, 256), 1e-6),
+])
+def test_task1_gpu_binary(gpu, binary, shape, bound):
+    m, n, k = shape
+    announce(f"{binary} -m {m} -n {n} -k {k}")
+    p = subprocess.run([os.path.join(BIN, binary), "-m", str(m), "-n", str(n), "-k", str(k), "-w", "2",
+                        "-t", "5", "--json"], capture_output=True, text=True, timeout=120)
+    assert p.returncode == 0, p.stderr
+    res = RESULT_RE.search(p.stdout)
+    assert res, p.stdout
+    assert float(res.group("tf")) > 0
+    assert float(res.group("err")) < bound
+    assert '"iters": 5' in p.stdout
+
+
+def test_bench_loops(gpu):
+    import torch
+    import vibekernel_amd as vk
+    import bench
+    L = bench.load_bench_lib()
+    m = n = k = 1024
+    A = torch.rand((m, k), device="cuda:0").half()
+    B = torch.rand((k, n), device="cuda:0").half()
+    C = torch.empty((m, n), dtype=torch.float16, device="cuda:0")
+    s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+    call = (3, vk.DTYPE_F16, vk.DTYPE_F16, m, n, k, ctypes.c_void_p(A.data_ptr()), ctypes.c_void_p(B.data_ptr()),
+            ctypes.c_void_p(C.data_ptr()), s)
+    per = (ctypes.c_float * 7)()
+    announce("bench loops v3 1024^3")
+    assert L.vkb_reference_loop(*call, 2, 7, per) == 0
+    assert all(x > 0 for x in per)
+    tot = ctypes.c_float(0)
+    assert L.vkb_back_to_back(*call, 5, ctypes.byref(tot)) == 0 and tot.value > 0
+    ref = torch.matmul(A.float(), B.float())
+    # fp16 output: within half an fp16 ulp (2^-11 relative) plus fp32 noise
+    assert float(((C.float() - ref).abs() / ref.abs().clamp_min(1.0)).max()) < 1e-3
+    # an invalid call reports its status instead of launching
+    bad = (3, vk.DTYPE_F16, vk.DTYPE_F16, 1000, n, k) + call[6:]
+    assert L.vkb_reference_loop(*bad, 0, 1, per) == -3
