@@ -197,16 +197,33 @@ def main():
 
     peak = PEAK_F16_TFLOPS if dtype == "f16" else PEAK_F32_TFLOPS
     workload = f"gemm_{dtype}_{m}x{n}x{k}"
-    roofline = {
-        "bound": "mfma" if dtype == "f16" else "valu",
-        "achieved": round(tflops, 2),
-        "peak": peak,
-        "unit": "TFLOP/s",
-        "frac": round(tflops / peak, 4),
-        "traffic": read_traffic(kname, workload),
-        "kernel": kname,
-        "algorithmic_flop_per_launch": flop,
-    }
+    esz = 2 if dtype == "f16" else 4
+    algo_bytes = (m * k + k * n) * esz + m * n * (2 if out == "f16" else 4)
+    intensity = flop / algo_bytes
+    if intensity < peak * 1e12 / (PEAK_HBM_GBS * 1e9):
+        # below the ridge point: the bound is HBM bandwidth
+        gbs = algo_bytes / (mean_ms * 1e-3) / 1e9
+        roofline = {
+            "bound": "hbm",
+            "achieved": round(gbs, 1),
+            "peak": PEAK_HBM_GBS,
+            "unit": "GB/s",
+            "frac": round(gbs / PEAK_HBM_GBS, 4),
+            "traffic": read_traffic(kname, workload),
+            "kernel": kname,
+            "algorithmic_bytes_per_launch": algo_bytes,
+        }
+    else:
+        roofline = {
+            "bound": "mfma" if dtype == "f16" else "valu",
+            "achieved": round(tflops, 2),
+            "peak": peak,
+            "unit": "TFLOP/s",
+            "frac": round(tflops / peak, 4),
+            "traffic": read_traffic(kname, workload),
+            "kernel": kname,
+            "algorithmic_flop_per_launch": flop,
+        }
     res = {
         "metric": METRIC,
         "value": round(tflops, 2),

@@ -18,6 +18,7 @@ pytestmark = pytest.mark.gpu
 
 TILE_SHAPES = [(256, 256, 64), (512, 256, 128), (256, 512, 192), (768, 512, 256), (1024, 1024, 512)]
 ANY_SHAPES = [(1, 1, 1), (17, 33, 65), (127, 129, 31), (200, 300, 100), (256, 256, 64), (64, 8, 1000)]
+SKINNY_SHAPES = [(16, 256, 512), (32, 512, 1024), (48, 96, 128), (64, 128, 256), (16, 2048, 4096)]
 
 
 def _versions():
@@ -31,6 +32,9 @@ def _shapes_for(version):
     shapes = [s for s in TILE_SHAPES if s[0] % c.div_m == 0 and s[1] % c.div_n == 0 and s[2] % c.div_k == 0]
     if c.div_m == 1 and c.div_n == 1 and c.div_k == 1:
         shapes = ANY_SHAPES + shapes[:2]
+    if c.max_m <= 64:
+        shapes = [s for s in SKINNY_SHAPES if s[0] <= c.max_m and s[0] % c.div_m == 0
+                  and s[1] % c.div_n == 0 and s[2] % c.div_k == 0]
     return shapes
 
 
@@ -183,3 +187,29 @@ def test_repeat_launch_deterministic(gpu, version):
         vk.matmul(m, n, k, A, B, C, version)
         assert torch.equal(C, ref)
     torch.cuda.synchronize()
+
+
+@pytest.mark.slow
+def test_skinny_decode_shape(gpu, oracle):
+    """M = 16, N = K = 8192 (the decode-like, HBM-bound configuration) on the
+    skinny kernel, fp16 and fp32 output, against the oracle."""
+    m, n, k = 16, 8192, 8192
+    A, B = make_inputs(m, n, k, "uniform", seed=16)
+    C64 = oracle.dgemm(A, B)
+    C32 = run_gemm(4, A, B, "f32")
+    check_f32_out(C32, A, B, C64)
+    C16 = run_gemm(4, A, B, "f16")
+    check_f16_out(C16, A, B, C64)
+    err, st = oracle.mean_rel_err(oracle.hgemm(A, B), C16)
+    assert st == oracle.STATUS_OK and err < 2e-4
+
+
+def test_skinny_rejects_wide_m(gpu):
+    import torch
+    import vibekernel_amd as vk
+    A = torch.zeros((80, 128), dtype=torch.float16, device="cuda:0")
+    B = torch.zeros((128, 64), dtype=torch.float16, device="cuda:0")
+    C = torch.zeros((80, 64), dtype=torch.float16, device="cuda:0")
+    with pytest.raises(vk.VkError) as e:
+        vk.matmul(80, 64, 128, A, B, C, 4)
+    assert e.value.status == -3

@@ -53,6 +53,13 @@ __device__ __forceinline__ half4 lds_read_tr16(const half_t* lds_addr) {
   return __builtin_bit_cast(half4, r);
 }
 
+// Same, from a 32-bit LDS byte address (no generic-pointer round trip).
+__device__ __forceinline__ half4 lds_read_tr16_at(uint32_t lds_byte_addr) {
+  short4v r = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) short4v*)(uintptr_t)lds_byte_addr);
+  return __builtin_bit_cast(half4, r);
+}
+
 // 16 bytes from global straight into LDS at lds_wave_base + 16 * lane.
 __device__ __forceinline__ void global_load_lds16(const void* gptr, void* lds_wave_base) {
   __builtin_amdgcn_global_load_lds(gptr, VK_LDS_PTR(void, lds_wave_base), 16, 0, 0);
