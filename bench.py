@@ -4,18 +4,36 @@
 Workload (the reference's scored configuration, results/ralph_loop_fable/src/
 main.cpp:43-62 and :83-90): C = A . B, A and B fp16 4096x4096 row-major,
 fp32 accumulation, fp16 C; synthetic uniform[-1,1) inputs from a fixed seed,
-already resident in HBM.  Timing follows the reference loop exactly:
-`--warmup` untimed launches, then `--steps` launches each bracketed by its own
-event pair on the kernel's stream and a host sync; the reported value is
-2*m*n*k / mean(launch time).  The whole timed loop is itself bracketed by
-device synchronisations.
+already resident in HBM.
+
+Before the timed region the GEMM runs back to back, untimed, for `--settle-ms`
+(default 300 ms): under a sustained matrix-core load MI355X starts at a
+reduced clock (about 1.37 GHz for this GEMM) and raises it over some tens of
+milliseconds to its sustained, power-limited level (about 1.6 GHz); the
+reference's 10 warm-up launches (about 1.3 ms here) would leave the timed
+launches inside that ramp.
+
+Timed region: `--warmup` untimed launches, a device synchronisation, then
+`--steps` launches back to back on the kernel's stream between one HIP event
+pair, then a device synchronisation (all in C++, libvk_bench.so).
+ms_per_step = event time / steps (the mean launch duration);
+value = 2*m*n*k / ms_per_step.  The reference's
+own loop (an event pair and a host sync around every launch, main.cpp:52-62)
+runs afterwards with `--reference-loop` and is reported as `reference_loop`.
+The two differ on MI355X: back to back, the GEMM holds the board at its power
+limit and the clock drops; the idle gaps of the synchronised loop let it
+recover, so its per-launch times are shorter.
+
+Other configurations of the same GEMM: `--workload` (see WORKLOADS) or
+explicit --m/--n/--k/--dtype/--dist.
 
 Prints ONE JSON line.  Extra objects:
-  roofline     -- achieved TFLOP/s of the kernel vs the MI355X dense fp16 MFMA
-                  peak; `traffic` (HBM bytes per launch) from the committed
-                  rocprofv3 counter summary in profiles/, else null;
+  roofline     -- the kernel against its bound: dense fp16 MFMA peak (TFLOP/s),
+                  or HBM bandwidth (GB/s) when the GEMM's arithmetic intensity
+                  is below the ridge point; `traffic` (HBM bytes per launch) from
+                  the committed rocprofv3 counter summary in profiles/, else null;
   cpu_baseline -- the CPU oracle's v0 path (widen, cblas-style sgemm, narrow)
-                  timed on this host's cores on the same workload.
+                  timed on this host's cores on a bounded sample of the workload.
 """
 from __future__ import annotations
 
@@ -34,6 +52,21 @@ PEAK_F32_TFLOPS = 157.3    # published fp32 figure (the VALU kernel reaches at m
 PEAK_HBM_GBS = 8000.0
 METRIC = "sustained fp16 GEMM TFLOPS at 4096³ (100-iter avg) + % of MFMA peak"
 
+# name -> (m, n, k, dtype, dist)
+WORKLOADS = {
+    "square4096": (4096, 4096, 4096, "f16", "uniform"),       # the headline
+    "square4096_normal": (4096, 4096, 4096, "f16", "normal"),  # reference-parity N(0,1) inputs
+    "mlp_up": (4096, 11008, 4096, "f16", "uniform"),
+    "mlp_down": (4096, 4096, 11008, "f16", "uniform"),
+    "square8192": (8192, 8192, 8192, "f16", "normal0.5"),
+    "skinny": (16, 8192, 8192, "f16", "uniform"),
+    "f32_4096": (4096, 4096, 4096, "f32", "uniform"),
+    "f32_512": (512, 512, 512, "f32", "uniform"),
+}
+
+
+DIST_TEXT = {"uniform": "uniform[-1,1)", "normal": "N(0,1)", "normal0.5": "N(0,0.5)"}
+
 
 def parse():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
@@ -41,16 +74,32 @@ def parse():
     p.add_argument("--steps", type=int, default=100)
     p.add_argument("--warmup", type=int, default=10)
     p.add_argument("--version", type=int, default=None, help="kernel version (default: the library default)")
-    p.add_argument("--m", type=int, default=4096)
-    p.add_argument("--n", type=int, default=4096)
-    p.add_argument("--k", type=int, default=4096)
-    p.add_argument("--dtype", choices=["f16", "f32"], default="f16")
+    p.add_argument("--workload", choices=sorted(WORKLOADS), default="square4096")
+    p.add_argument("--m", type=int, default=None)
+    p.add_argument("--n", type=int, default=None)
+    p.add_argument("--k", type=int, default=None)
+    p.add_argument("--dtype", choices=["f16", "f32"], default=None)
+    p.add_argument("--dist", choices=["uniform", "normal", "normal0.5"], default=None)
     p.add_argument("--out", choices=["f16", "f32"], default=None)
     p.add_argument("--seed", type=int, default=20261201)
     p.add_argument("--cpu-seconds", type=float, default=12.0,
                    help="CPU baseline budget (repeats of the v0 GEMM until this much time)")
     p.add_argument("--no-cpu-baseline", action="store_true")
-    return p.parse_args()
+    p.add_argument("--settle-ms", type=float, default=300.0,
+                   help="run the GEMM back to back for this long before the warm-up (untimed): "
+                        "MI355X starts a sustained matrix-core load at a reduced clock and raises "
+                        "it to its sustained level over some tens of milliseconds")
+    p.add_argument("--reference-loop", action="store_true",
+                   help="also run the reference's per-launch synchronised loop after the timed region "
+                        "(more launches of the same kernel: leave off under a profiler)")
+    a = p.parse_args()
+    m, n, k, dt, dist = WORKLOADS[a.workload]
+    a.m = a.m or m
+    a.n = a.n or n
+    a.k = a.k or k
+    a.dtype = a.dtype or dt
+    a.dist = a.dist or dist
+    return a
 
 
 def read_traffic(kernel_name: str, workload: str):
@@ -86,15 +135,24 @@ def load_bench_lib():
     L.vkb_back_to_back.argtypes = [ci, ci, ci, sz, sz, sz, vp, vp, vp, vp, ci,
                                    ctypes.POINTER(ctypes.c_float)]
     L.vkb_back_to_back.restype = ci
+    fp = ctypes.POINTER(ctypes.c_float)
+    L.vkb_stream_loop.argtypes = [ci, ci, ci, sz, sz, sz, vp, vp, vp, vp, ci, ci, fp]
+    L.vkb_stream_loop.restype = ci
     return L
 
 
 def cpu_baseline(m, n, k, dtype, seed, budget_s):
     """The oracle's v0 restatement (test infrastructure) timed on this host:
     fp16 -> widen, sgemm, narrow (matmul_f16_v0_cblas.cpp:13-25); repeats the
-    full GEMM until `budget_s` seconds have been spent (at least once)."""
+    GEMM until `budget_s` seconds have been spent (at least once).  Beyond
+    2^38 FLOP the sample is a row band of A (same n and k, fewer rows): the
+    rate per FLOP of a blocked SGEMM does not depend on the row count once it
+    spans many cache blocks."""
     import numpy as np
     from oracle import oracle as O
+    full_m = m
+    while 2.0 * m * n * k > 2.0 ** 38 and m % 2 == 0 and m > 256:
+        m //= 2
     rng = np.random.default_rng(seed)
     if dtype == "f16":
         A = rng.uniform(-1, 1, (m, k)).astype(np.float16)
@@ -118,7 +176,8 @@ def cpu_baseline(m, n, k, dtype, seed, budget_s):
         "unit": "TFLOPS",
         "cores": O.num_threads(),
         "kind": "port",
-        "sample": (f"full {m}x{n}x{k} {dtype} GEMM through the oracle's v0 path "
+        "sample": (("full " if m == full_m else f"{m}-row band of the {full_m}-row ") +
+                   f"{m}x{n}x{k} {dtype} GEMM through the oracle's v0 path "
                    f"(OpenMP sgemm, fp32 fmaf accumulation), {reps} repeat(s), "
                    f"{el:.1f} s, {per * 1e3:.1f} ms per GEMM"),
     }
@@ -143,7 +202,7 @@ def main():
     m, n, k = args.m, args.n, args.k
     dtype = args.dtype
     out = args.out or dtype
-    version = args.version if args.version is not None else (vk.DEFAULT_F16_VERSION if dtype == "f16" else 1)
+    version = args.version if args.version is not None else vk.pick_version(m, n, k, dtype, out)
     kname = vk.name(version, dtype)
     if kname is None:
         print(f"bench.py: unknown {dtype} version {version}", file=sys.stderr)
@@ -152,8 +211,18 @@ def main():
     tdt = torch.float16 if dtype == "f16" else torch.float32
     odt = torch.float16 if out == "f16" else torch.float32
     g = torch.Generator(device=dev).manual_seed(args.seed)
-    A = (torch.rand((m, k), generator=g, device=dev, dtype=torch.float32) * 2 - 1).to(tdt)
-    B = (torch.rand((k, n), generator=g, device=dev, dtype=torch.float32) * 2 - 1).to(tdt)
+
+    def draw(shape):
+        if args.dist == "uniform":
+            x = torch.rand(shape, generator=g, device=dev, dtype=torch.float32) * 2 - 1
+        else:
+            x = torch.randn(shape, generator=g, device=dev, dtype=torch.float32)
+            if args.dist == "normal0.5":
+                x = x * 0.5
+        return x.to(tdt)
+
+    A = draw((m, k))
+    B = draw((k, n))
     C = torch.empty((m, n), dtype=odt, device=dev)
     stream = torch.cuda.current_stream(dev)
 
@@ -164,31 +233,51 @@ def main():
     call = (version, in_code, out_code, m, n, k, ctypes.c_void_p(A.data_ptr()),
             ctypes.c_void_p(B.data_ptr()), ctypes.c_void_p(C.data_ptr()), sptr)
 
-    # Timed region: the reference loop (main.cpp:52-62) run in C++ on the
-    # kernel's stream: warm-up calls, then each call between its own event
-    # pair with a host sync.  Bracketed by device synchronisations.
-    per = (ctypes.c_float * args.steps)()
+    # Untimed settle phase: back-to-back launches until the clock has reached
+    # its sustained level (see --settle-ms).
+    settle_launches = 0
+    if args.settle_ms > 0:
+        probe = ctypes.c_float(0.0)
+        st = bench.vkb_back_to_back(*call, 5, ctypes.byref(probe))
+        if st != 0:
+            print(f"bench.py: settle phase failed with status {st}", file=sys.stderr)
+            return 1
+        settle_launches = max(1, int(args.settle_ms / max(probe.value / 5, 1e-3)))
+        st = bench.vkb_back_to_back(*call, settle_launches, ctypes.byref(probe))
+        if st != 0:
+            print(f"bench.py: settle phase failed with status {st}", file=sys.stderr)
+            return 1
+        settle_launches += 5
+
+    # Timed region (C++, on the kernel's stream): warm-up, device sync, then
+    # `steps` launches back to back between one event pair, device sync.
+    # Wall clock around it as a cross-check.
+    tot = ctypes.c_float(0.0)
     torch.cuda.synchronize()
     w0 = time.perf_counter()
-    st = bench.vkb_reference_loop(*call, args.warmup, args.steps, per)
+    st = bench.vkb_stream_loop(*call, args.warmup, args.steps, ctypes.byref(tot))
     torch.cuda.synchronize()
     wall = time.perf_counter() - w0
     if st != 0:
-        print(f"bench.py: reference loop failed with status {st}", file=sys.stderr)
+        print(f"bench.py: timed loop failed with status {st}", file=sys.stderr)
         return 1
-    per_ms = list(per)
-    mean_ms = sum(per_ms) / len(per_ms)
+    mean_ms = tot.value / args.steps
     flop = 2.0 * m * n * k
     tflops = flop / (mean_ms * 1e-3) / 1e12
 
-    # Diagnostic after the timed region: back-to-back launches between one
-    # event pair (no host sync in between).
-    tot = ctypes.c_float(0.0)
-    st = bench.vkb_back_to_back(*call, args.steps, ctypes.byref(tot))
-    if st != 0:
-        print(f"bench.py: back-to-back loop failed with status {st}", file=sys.stderr)
-        return 1
-    b2b_ms = tot.value / args.steps
+    # Optionally, after the timed region: the reference's loop (event pair and
+    # host sync around every launch, main.cpp:52-62), reported beside the value.
+    ref_loop = None
+    if args.reference_loop:
+        ref_n = min(args.steps, 100)
+        ref_per = (ctypes.c_float * ref_n)()
+        st = bench.vkb_reference_loop(*call, 2, ref_n, ref_per)
+        if st != 0:
+            print(f"bench.py: reference loop failed with status {st}", file=sys.stderr)
+            return 1
+        ref_ms = sum(ref_per) / ref_n
+        ref_loop = {"iters": ref_n, "mean_ms": round(ref_ms, 5), "min_ms": round(min(ref_per), 5),
+                    "max_ms": round(max(ref_per), 5), "tflops": round(flop / (ref_ms * 1e-3) / 1e12, 2)}
 
     # Sanity of the timed output against torch's own GEMM (fp32 accumulate);
     # the parity tests hold the real oracle comparison.
@@ -240,18 +329,17 @@ def main():
         "data": "synthetic",
         "config": {
             "workload": f"{workload} row-major NN, fp32 accumulate, {out} out, "
-                        f"uniform[-1,1) seed {args.seed}",
+                    f"{DIST_TEXT[args.dist]} seed {args.seed}",
+            "preset": args.workload,
             "m": m, "n": n, "k": k,
             "version": version,
             "kernel": kname,
             "out_dtype": out,
         },
         "pct_of_peak": round(100.0 * tflops / peak, 2),
-        "wall_ms_per_step": round(wall * 1e3 / args.steps, 5),
-        "backtoback_ms_per_launch": round(b2b_ms, 5),
-        "backtoback_tflops": round(flop / (b2b_ms * 1e-3) / 1e12, 2),
-        "min_ms": round(min(per_ms), 5),
-        "max_ms": round(max(per_ms), 5),
+        "wall_ms_per_step": round(wall * 1e3 / (args.steps + args.warmup), 5),
+        "settle": {"ms": args.settle_ms, "launches": settle_launches},
+        "reference_loop": ref_loop,
         "max_abs_vs_torch_f32": max_abs_vs_torch,
         "reference_best_a100_frac_of_peak": 0.897,
         "roofline": roofline,

@@ -32,6 +32,17 @@ int vkb_back_to_back(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t 
                      size_t k, const void* A, const void* B, void* C, void* stream, int iters,
                      float* total_ms);
 
+/* The benchmark's timed region on `stream`: `warmup` untimed calls, a device
+ * synchronisation, then `iters` calls back to back between one event pair (no
+ * host sync in between), then a device synchronisation; *total_ms receives
+ * the elapsed time between the events.  An event recorded between every pair
+ * of calls would not do: on ROCm each such record lengthens the launch that
+ * follows it.  Not in the reference, whose loop syncs the host after every
+ * call (vkb_reference_loop). */
+int vkb_stream_loop(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, size_t n,
+                    size_t k, const void* A, const void* B, void* C, void* stream, int warmup,
+                    int iters, float* total_ms);
+
 #ifdef __cplusplus
 }
 #endif

@@ -95,3 +95,12 @@ def test_single_hip_runtime_in_process():
     from vibekernel_amd import _abi
     _abi.load()
     assert len(_abi.hip_runtimes_loaded()) == 1, _abi.hip_runtimes_loaded()
+
+
+def test_pick_version_follows_shape():
+    import vibekernel_amd as vk
+    assert vk.pick_version(16, 8192, 8192) == 4
+    assert vk.pick_version(4096, 4096, 4096) == 5
+    assert vk.pick_version(4096, 4096, 4096, "f16", "f32") == 5
+    assert vk.pick_version(100, 300, 70) == 1
+    assert vk.pick_version(512, 512, 512, "f32") == 1

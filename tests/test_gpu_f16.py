@@ -125,7 +125,7 @@ def test_rejected_shape_raises_before_launch(gpu):
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("version", [2, 3])
+@pytest.mark.parametrize("version", [2, 3, 5])
 def test_headline_4096_reference_metric(gpu, oracle, version):
     """4096^3 on the reference's own input distribution (N(0,1)) and metric
     (mean relative error of the fp16 C, test_data.hpp:145-162).
@@ -153,7 +153,7 @@ def test_headline_4096_reference_metric(gpu, oracle, version):
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("version", [2, 3])
+@pytest.mark.parametrize("version", [2, 3, 5])
 def test_headline_4096_f32_out(gpu, oracle, version):
     m = n = k = 4096
     A, B = make_inputs(m, n, k, "uniform", seed=7)
@@ -167,7 +167,7 @@ def test_headline_4096_f32_out(gpu, oracle, version):
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("version", [2, 3])
+@pytest.mark.parametrize("version", [2, 3, 5])
 def test_repeat_launch_deterministic(gpu, version):
     """110 launches (the reference caught its cp.async race only after >=110
     runs): C poisoned with NaN before each launch, every result bitwise equal
@@ -187,6 +187,49 @@ def test_repeat_launch_deterministic(gpu, version):
         vk.matmul(m, n, k, A, B, C, version)
         assert torch.equal(C, ref)
     torch.cuda.synchronize()
+
+
+@pytest.mark.slow
+def test_square8192_normal05(gpu, oracle):
+    """8192^3 on N(0, 0.5) inputs (the configuration of the reference's
+    fp16-accumulate tier, matmul_f16_v14_f16acc.cu; CDNA4 accumulates in fp32,
+    so the strict checks apply): fp32 output within the fp32 accumulation
+    bound of the oracle; fp16 output bit-identical to the RNE rounding of the
+    kernel's own fp32 output; reference statistic against v0 below the
+    relaxed tier's 1e-3."""
+    import vibekernel_amd as vk
+    version = vk.DEFAULT_F16_VERSION
+    m = n = k = 8192
+    A, B = make_inputs(m, n, k, "normal0.5", seed=8192)
+    C32 = run_gemm(version, A, B, "f32")
+    C16 = run_gemm(version, A, B, "f16")
+    assert np.array_equal(C16.view(np.uint16), C32.astype(np.float16).view(np.uint16))
+    Corc = oracle.hgemm(A, B, out="f32")
+    absAB = oracle.sgemm(np.abs(A.astype(np.float32)), np.abs(B.astype(np.float32)))
+    diff = np.abs(C32.astype(np.float64) - Corc)
+    assert np.all(diff <= 2 * 2 * k * 2.0 ** -24 * absAB.astype(np.float64))
+    del absAB, diff
+    err, st = oracle.mean_rel_err(Corc.astype(np.float16), C16)
+    print(f"v{version} 8192^3 N(0,0.5): mean-rel vs v0 {err:.3e}")
+    assert st == oracle.STATUS_OK and err < 1e-3
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("shape", [(4096, 11008, 4096), (4096, 4096, 11008)])
+def test_mlp_shapes(gpu, oracle, shape):
+    """The MLP projections (688 tiles of 256 x 256: 2.69 waves on 256 CUs):
+    default version, fp32 output against the oracle within the fp32
+    accumulation bound, fp16 output equal to its rounding."""
+    import vibekernel_amd as vk
+    version = vk.DEFAULT_F16_VERSION
+    m, n, k = shape
+    A, B = make_inputs(m, n, k, "uniform", seed=11008)
+    C32 = run_gemm(version, A, B, "f32")
+    C16 = run_gemm(version, A, B, "f16")
+    assert np.array_equal(C16.view(np.uint16), C32.astype(np.float16).view(np.uint16))
+    Corc = oracle.hgemm(A, B, out="f32")
+    absAB = oracle.sgemm(np.abs(A.astype(np.float32)), np.abs(B.astype(np.float32)))
+    assert np.all(np.abs(C32.astype(np.float64) - Corc) <= 2 * 2 * k * 2.0 ** -24 * absAB.astype(np.float64))
 
 
 @pytest.mark.slow

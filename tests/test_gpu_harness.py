@@ -20,6 +20,8 @@ RESULT_RE = re.compile(r"TFLOPS: (?P<tf>[0-9.eE+-]+); *Average Error: (?P<err>[0
     ("task1_float16_v1", (512, 512, 512), 2e-4),
     ("task1_float16_v2", (1024, 512, 256), 2e-4),
     ("task1_float16_v3", (1024, 1024, 1024), 2e-4),
+    ("task1_float16_v4", (32, 1024, 2048), 2e-4),
+    ("task1_float16_v5", (1024, 768, 512), 2e-4),
     ("task1_float32_v1", (512, 384, 256), 1e-6),
 ])
 def test_task1_gpu_binary(gpu, binary, shape, bound):
@@ -53,6 +55,9 @@ def test_bench_loops(gpu):
     assert all(x > 0 for x in per)
     tot = ctypes.c_float(0)
     assert L.vkb_back_to_back(*call, 5, ctypes.byref(tot)) == 0 and tot.value > 0
+    tot = ctypes.c_float(0)
+    assert L.vkb_stream_loop(*call, 2, 5, ctypes.byref(tot)) == 0 and tot.value > 0
+    assert L.vkb_stream_loop(*call, 0, 0, ctypes.byref(tot)) == -3  # no timed launches: rejected
     ref = torch.matmul(A.float(), B.float())
     # fp16 output: within half an fp16 ulp (2^-11 relative) plus fp32 noise
     assert float(((C.float() - ref).abs() / ref.abs().clamp_min(1.0)).max()) < 1e-3

@@ -5,8 +5,8 @@ include/vk_gemm.h); this package is the Python front end used by the tests
 and the benchmark.
 """
 from ._abi import DTYPE_F16, DTYPE_F32, VkError, abi_version, lib_path, load  # noqa: F401
-from .gemm import gemm, matmul, name, query, versions  # noqa: F401
+from .gemm import gemm, matmul, name, pick_version, query, versions  # noqa: F401
 
 # Default fp16 version: the fastest kernel for tile-divisible shapes (256x256 tiles,
-# BK=32, 4-stage direct-to-LDS ring).
-DEFAULT_F16_VERSION = 3
+# BK=32, 4-stage direct-to-LDS ring, 8 waves in two phase-shifted groups).
+DEFAULT_F16_VERSION = 5

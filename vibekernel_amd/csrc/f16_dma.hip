@@ -23,6 +23,7 @@
 //    so they share A and B panels in that XCD's L2.
 #include "vk_device.hpp"
 #include "vk_internal.hpp"
+#include "vk_tile.hpp"
 
 #include <atomic>
 #include <type_traits>
@@ -34,72 +35,6 @@ constexpr int kBM = 256;
 constexpr int kBN = 256;
 constexpr int kThreads = 256;
 constexpr int kWaves = 4;
-
-// A rows are BK halves = BK/8 chunks of 16 B.  Swizzle of the chunk index as a
-// function of the row, chosen so the 16-byte A-fragment reads of consecutive
-// rows hit distinct banks.
-template <int BK>
-__host__ __device__ constexpr int swz_a(int row) {
-  if constexpr (BK == 64) {
-    return (row & 7) ^ ((row >> 3) & 1);
-  } else {  // BK == 32: 4 chunks per row
-    return ((row >> 1) & 3) ^ ((row >> 2) & 3);
-  }
-}
-
-// B rows are 256 halves = 32 chunks.  The transpose reads touch 4 consecutive
-// k rows x 2 or 4 neighbouring chunks per 16 or 32 lanes; XOR by v[k % 4]
-// spreads them over distinct banks.
-__host__ __device__ constexpr int swz_b(int krow) {
-  return (krow & 3) == 0 ? 0 : (krow & 3) == 1 ? 6 : (krow & 3) == 2 ? 12 : 10;
-}
-
-// s_waitcnt with only a vmcnt limit (gfx9 encoding: vmcnt[3:0], expcnt[6:4],
-// lgkmcnt[11:8], vmcnt[5:4] at [15:14]).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
-
-// Workgroup barrier for LDS producer/consumer hand-off only: waits for this
-// wave's LDS reads (lgkmcnt) but, unlike __syncthreads(), not for its
-// in-flight global->LDS prefetches (vmcnt), which are waited for explicitly.
-// The "memory" clobbers keep the compiler from moving LDS accesses across it.
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
-}
-
-// 32-bit LDS address of a pointer into workgroup memory.
-__device__ __forceinline__ uint32_t lds_addr32(const void* p) {
-  return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const char*)p);
-}
-
-// Direct-to-LDS load: lane l's 16 bytes at gbase + voff land at LDS address
-// lds_dst + 16 * l (lds_dst and gbase are wave-uniform).  Issued as inline
-// asm so the compiler does not track it: it would otherwise treat every later
-// LDS transpose read as aliasing the pending DMA and wait for all of them
-// (vmcnt(0)), which would drain the prefetch ring.  Completion is awaited
-// explicitly with wait_vmcnt().  Nothing else in these kernels uses M0.
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-__device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t lds_dst) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :
-               : "s"(lds_dst), "v"(voff), "s"(gbase)
-               : "m0");
-}
-#pragma clang diagnostic pop
-
-// 4 consecutive outputs, one vector store (8 B for fp16, 16 B for fp32).
-__device__ __forceinline__ void store4(half_t* p, float a, float b, float c, float d) {
-  half4 h = {(half_t)a, (half_t)b, (half_t)c, (half_t)d};
-  *reinterpret_cast<half4*>(p) = h;
-}
-__device__ __forceinline__ void store4(float* p, float a, float b, float c, float d) {
-  float4v f = {a, b, c, d};
-  *reinterpret_cast<float4v*>(p) = f;
-}
 
 template <int BK, int NSTAGE>
 struct Cfg {
@@ -117,34 +52,9 @@ struct Cfg {
   static_assert(kLdsBytes >= 4 * 128 * 128 * 2, "epilogue staging needs 128 KB");
 };
 
-// Tile order: XCD-aware remap plus a grouped raster of GM tile-rows.
-__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int total = tiles_m * tiles_n;
-  int cid = bid;
-  if ((total & 7) == 0) cid = (bid & 7) * (total >> 3) + (bid >> 3);
-  constexpr int GM = 4;
-  const int group = GM * tiles_n;
-  const int g = cid / group;
-  const int first_m = g * GM;
-  const int gm = min(tiles_m - first_m, GM);
-  const int r = cid - g * group;
-  tm = first_m + r % gm;
-  tn = r / gm;
-}
-
 // LDS bytes each wave uses to stage its 128x128 output block (fp16: the whole
 // block; fp32: half of it per pass).
 constexpr int kEpiWaveBytes = 128 * 128 * 2;
-
-__device__ __forceinline__ void lds_write8(uint32_t addr, half4 v) {
-  *reinterpret_cast<__attribute__((address_space(3))) half4*>(addr) = v;
-}
-__device__ __forceinline__ void lds_write16(uint32_t addr, float4v v) {
-  *reinterpret_cast<__attribute__((address_space(3))) float4v*>(addr) = v;
-}
-__device__ __forceinline__ uint4v lds_read16(uint32_t addr) {
-  return *reinterpret_cast<const __attribute__((address_space(3))) uint4v*>(addr);
-}
 
 // fp16 output: the wave's 128x128 block, row pitch 256 B = 16 chunks of 16 B,
 // physical chunk = chunk ^ (row % 16).  Read back 4 rows per instruction.
@@ -201,7 +111,7 @@ epilogue_store(float16v (&acc)[4][4], char*, uint32_t wbase, OutT* Cw, int N, in
       const uint4v v = lds_read16(wbase + row * 512 + 16 * (ch ^ (row & 31)));
       *reinterpret_cast<uint4v*>(Cw + (size_t)(pass * 64 + row) * N + ch * 4) = v;
     }
-    if (pass == 0) __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0): region reused next pass
+    if (pass == 0) wait_lgkmcnt0();  // region reused next pass
   }
 }
 
@@ -382,18 +292,6 @@ __global__ __launch_bounds__(kThreads, 1) void f16_dma_kernel(const half_t* __re
   lds_barrier();
   epilogue_store<OutT>(acc, lds + wave * kEpiWaveBytes, lds_addr32(lds) + wave * kEpiWaveBytes,
                        C + (size_t)(m0 + wm * 128) * N + n0 + wn * 128, N, lane);
-}
-
-// hipFuncSetAttribute(MaxDynamicSharedMemorySize) once per kernel instance
-// and device (a bit per device id).
-template <typename KFn>
-hipError_t ensure_lds_attr(KFn kfn, int bytes, int device, std::atomic<uint64_t>& done) {
-  const uint64_t bit = device < 64 ? (1ull << device) : 0;
-  if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
-  hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kfn),
-                                     hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
-  if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_acq_rel);
-  return e;
 }
 
 template <int BK, int NSTAGE, typename OutT>

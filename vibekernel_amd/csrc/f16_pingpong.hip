@@ -1,0 +1,307 @@
+// f16_pingpong.hip -- fp16 GEMM, version 5: 256x256 tile, 8 waves in two
+// phase-shifted groups ("ping-pong").
+//
+// Same job and tile as version 3 (f16_dma.hip; the reference's champion is
+// results/ralph_loop_fable/src/matmul_f16/matmul_f16_v42_shfl2.cu:104-490),
+// but with two waves per SIMD instead of one.  A 512-thread workgroup places
+// waves w and w + 4 on the same SIMD, so the waves form two groups, P = waves
+// 0..3 and Q = waves 4..7, one wave of each per SIMD:
+//
+//  * P computes rows 0..127 of the tile, Q rows 128..255; wave g of a group
+//    owns columns 64g..64g+63, i.e. a 128x64 block = 4x2 MFMA 32x32x16 blocks
+//    (128 fp32 accumulators per lane).
+//  * The k-loop alternates two phases separated by workgroup barriers:
+//      memory phase:  issue this wave's share of a future k-tile's
+//                     global->LDS loads and read the current k-tile's
+//                     fragments from LDS into registers;
+//      compute phase: 16 MFMAs on those fragments, nothing else.
+//    Q starts one phase later than P (one extra barrier at the start, P takes
+//    one at the end), so in every phase one wave of each SIMD issues only
+//    MFMAs while its partner reads LDS and issues loads: the matrix pipe is
+//    never left waiting on LDS latency, and a barrier costs only its own
+//    latency, hidden behind the MFMAs already issued.
+//  * LDS: a 4-stage ring of (A 256x32, B 32x256) k-tiles, 32 KB per stage,
+//    same swizzles as version 3.  P loads the B half of each k-tile and Q the
+//    A half, 4 direct-to-LDS instructions per wave per k-tile.
+//
+// Timeline (phase f = the interval between barriers f and f+1 after the
+// prologue barrier; t = k-tile):
+//    P: memory(t) in phase 2t,   compute(t) in phase 2t+1
+//    Q: memory(t) in phase 2t+1, compute(t) in phase 2t+2
+// Stage t % 4 is read in phases 2t (P) and 2t+1 (Q), so it is free from phase
+// 2t+2 on; memory(t) refills stage (t-1) % 4 with k-tile t+3.  Every wave
+// makes its loads of k-tile t+1 complete (vmcnt) before barrier 2t+2, the
+// first phase that reads that tile: P after compute(t), Q after memory(t).
+// Both groups pass the same number of barriers: 1 + 1 + 2 nk + 1.
+#include "vk_device.hpp"
+#include "vk_internal.hpp"
+#include "vk_tile.hpp"
+
+#include <atomic>
+#include <type_traits>
+
+namespace vk {
+namespace {
+
+constexpr int kBM = 256;
+constexpr int kBN = 256;
+constexpr int kBK = 32;
+constexpr int kNS = 4;  // LDS ring stages
+constexpr int kThreads = 512;
+constexpr int kABytes = kBM * kBK * 2;          // 16 KB
+constexpr int kBBytes = kBK * kBN * 2;          // 16 KB
+constexpr int kStageBytes = kABytes + kBBytes;  // 32 KB
+constexpr int kLdsBytes = kNS * kStageBytes;    // 128 KB
+constexpr int kDma = 4;                         // direct-to-LDS instructions per wave per k-tile
+// Outstanding loads allowed when k-tile t+1 must have landed: k-tiles t+2 ..
+// t+kNS-1 of this wave.
+constexpr int kVmWait = (kNS - 2) * kDma;
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+static_assert(kLdsBytes >= 8 * 128 * 64 * 2, "fp16 epilogue staging: 16 KB per wave");
+
+// fp16 output block of one wave (128 x 64) staged in LDS: row pitch 128 B = 8
+// chunks of 16 B; physical chunk = chunk ^ ((row / 2) % 8).  Rows r and r+1
+// fall in different halves of the 256-byte bank space, so the 32 rows a
+// column-wise write touches spread over 16 distinct 16-byte slots.
+__device__ __forceinline__ uint32_t epi16_addr(uint32_t base, int row, int chunk) {
+  return base + row * 128 + 16 * (chunk ^ ((row >> 1) & 7));
+}
+
+template <typename OutT>
+__device__ __forceinline__ typename std::enable_if<std::is_same<OutT, half_t>::value>::type
+epilogue_store(float16v (&acc)[4][2], uint32_t wbase, OutT* Cw, int N, int lane) {
+  // MFMA output of block (i, j) (C^T form, see the k-loop): lane l, register
+  // 4*g4 + e holds C[i*32 + l%32][j*32 + 8*g4 + 4*(l/32) + e].
+  const int r0 = lane & 31, hsel = lane >> 5;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int g4 = 0; g4 < 4; g4++) {
+        const int row = i * 32 + r0;
+        half4 h = {(half_t)acc[i][j][4 * g4 + 0], (half_t)acc[i][j][4 * g4 + 1],
+                   (half_t)acc[i][j][4 * g4 + 2], (half_t)acc[i][j][4 * g4 + 3]};
+        lds_write8(epi16_addr(wbase, row, 4 * j + g4) + 8 * hsel, h);
+      }
+  // Read back 8 rows x 8 chunks per instruction: each row a full 128-byte line.
+  const int rsub = lane >> 3, ch = lane & 7;
+#pragma unroll
+  for (int q = 0; q < 16; q++) {
+    const int row = 8 * q + rsub;
+    const uint4v v = lds_read16(epi16_addr(wbase, row, ch));
+    *reinterpret_cast<uint4v*>(Cw + (size_t)row * N + ch * 8) = v;
+  }
+}
+
+// fp32 output: two passes of 64 rows (16 KB per wave each), row pitch 256 B =
+// 16 chunks, physical chunk = chunk ^ (row % 16); 4 rows per read.
+template <typename OutT>
+__device__ __forceinline__ typename std::enable_if<std::is_same<OutT, float>::value>::type
+epilogue_store(float16v (&acc)[4][2], uint32_t wbase, OutT* Cw, int N, int lane) {
+  const int r0 = lane & 31, hsel = lane >> 5;
+#pragma unroll
+  for (int pass = 0; pass < 2; pass++) {
+#pragma unroll
+    for (int ii = 0; ii < 2; ii++)
+#pragma unroll
+      for (int j = 0; j < 2; j++)
+#pragma unroll
+        for (int g4 = 0; g4 < 4; g4++) {
+          const int i = 2 * pass + ii;
+          const int row = ii * 32 + r0;  // row within this pass
+          const int chunk = 8 * j + 2 * g4 + hsel;
+          float4v f = {acc[i][j][4 * g4 + 0], acc[i][j][4 * g4 + 1], acc[i][j][4 * g4 + 2],
+                       acc[i][j][4 * g4 + 3]};
+          lds_write16(wbase + row * 256 + 16 * (chunk ^ (row & 15)), f);
+        }
+    const int rsub = lane >> 4, ch = lane & 15;
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+      const int row = 4 * q + rsub;
+      const uint4v v = lds_read16(wbase + row * 256 + 16 * (ch ^ (row & 15)));
+      *reinterpret_cast<uint4v*>(Cw + (size_t)(pass * 64 + row) * N + ch * 4) = v;
+    }
+    if (pass == 0) wait_lgkmcnt0();  // this wave's region is rewritten by the next pass
+  }
+}
+
+template <typename OutT>
+__global__ __launch_bounds__(kThreads) void f16_pp_kernel(const half_t* __restrict__ A,
+                                                          const half_t* __restrict__ B,
+                                                          OutT* __restrict__ C, int M, int N, int K) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;  // 0 = P, 1 = Q; waves w and w+4 share a SIMD
+  const int gw = wave & 3;
+
+  int tm, tn;
+  tile_of(blockIdx.x, M / kBM, N / kBN, tm, tn);
+  const int m0 = tm * kBM, n0 = tn * kBN;
+  const uint32_t lds_base = lds_addr32(lds);
+
+  // ---- this wave's direct-to-LDS duty: P the B k-tile, Q the A k-tile ----
+  // A: instruction i covers rows gw*64 + i*16 .. +15 (4 chunks of 16 B each);
+  // B: instruction i covers k-rows gw*8 + 2i, +1 (32 chunks each).  Either way
+  // it lands at stage offset (grp ? 0 : kABytes) + (gw*4 + i) * 1024.
+  uint32_t doff[kDma];
+  const char* gsrc;
+  size_t gstep;  // bytes between consecutive k-tiles of the source
+  if (grp) {
+#pragma unroll
+    for (int i = 0; i < kDma; i++) {
+      const int row = gw * 64 + i * 16 + (lane >> 2);
+      const int c = (lane & 3) ^ swz_a<kBK>(row);
+      doff[i] = (uint32_t)(((size_t)row * K + c * 8) * 2);
+    }
+    gsrc = reinterpret_cast<const char*>(A) + (size_t)m0 * K * 2;
+    gstep = (size_t)kBK * 2;
+  } else {
+#pragma unroll
+    for (int i = 0; i < kDma; i++) {
+      const int krow = gw * 8 + i * 2 + (lane >> 5);
+      const int c = (lane & 31) ^ swz_b(krow);
+      doff[i] = (uint32_t)(((size_t)krow * N + c * 8) * 2);
+    }
+    gsrc = reinterpret_cast<const char*>(B) + (size_t)n0 * 2;
+    gstep = (size_t)kBK * N * 2;
+  }
+  const uint32_t ddst = (grp ? 0u : (uint32_t)kABytes) + gw * 4 * 1024;
+
+  // ---- fragment addresses (bytes inside a stage) ----
+  // A block i, k-step ks: row grp*128 + i*32 + lane%32, chunk 2*ks + lane/32.
+  const int arow = grp * 128 + (lane & 31);
+  uint32_t aoff[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ks++) aoff[ks] = arow * (kBK * 2) + 16 * ((2 * ks + (lane >> 5)) ^ swz_a<kBK>(arow));
+  // B block j, k-step ks, half h: lane 16g + 4jj + q names k-row
+  // ks*16 + 8*(g/2) + 4h + jj, columns gw*64 + j*32 + 16*(g%2) + 4q .. +3; the
+  // transpose read hands lane 16g + i the 4 k of column 16*(g%2) + i.
+  const int g = lane >> 4, jj = (lane >> 2) & 3, q = lane & 3;
+  uint32_t boff[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int krow0 = 8 * (g >> 1) + jj;  // plus ks*16 + 4h: krow0 % 4 is unchanged
+    const int c = gw * 8 + j * 4 + 2 * (g & 1) + (q >> 1);
+    boff[j] = kABytes + krow0 * (kBN * 2) + 16 * (c ^ swz_b(krow0)) + 8 * (q & 1);
+  }
+
+  float16v acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+  half8 fa[2][4], fb[2][2];
+  const int nk = K / kBK;
+
+  auto issue = [&](int stage, int kt) {
+    const uint32_t dst = lds_base + stage * kStageBytes + ddst;
+    const char* src = gsrc + (size_t)kt * gstep;
+#pragma unroll
+    for (int i = 0; i < kDma; i++) dma16(src, doff[i], dst + i * 1024);
+  };
+  auto read_frags = [&](int stage) {
+    const uint32_t sb = lds_base + stage * kStageBytes;
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) fa[ks][i] = lds_read_h8(sb + aoff[ks] + i * 32 * kBK * 2);
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const uint32_t p = sb + boff[j] + ks * 16 * kBN * 2;
+        const half4 lo = lds_read_tr16_at(p);
+        const half4 hi = lds_read_tr16_at(p + 4 * kBN * 2);
+        fb[ks][j] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+    }
+  };
+  // The B fragment is the MFMA's first operand, so each block computes C^T:
+  // lane l then holds 4 consecutive columns of row l % 32 (see the epilogue).
+  auto compute = [&]() {
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = mfma32x32x16(fb[ks][j], fa[ks][i], acc[i][j]);
+  };
+
+  // Prologue: k-tiles 0..kNS-2 in flight; tile 0 landed everywhere after the
+  // barrier.  Then Q takes one extra barrier so that it runs one phase behind.
+#pragma unroll
+  for (int s = 0; s < kNS - 1; s++) issue(s, min(s, nk - 1));
+  wait_vmcnt<kVmWait>();
+  lds_barrier();
+  if (grp) lds_barrier();
+
+  // Every iteration runs the same code for both groups; refills past the last
+  // k-tile are clamped to it and land in a stage that is never read again,
+  // which keeps the vmcnt bookkeeping constant.
+  for (int t = 0; t < nk; t++) {
+    __builtin_amdgcn_sched_barrier(0);
+    issue((t + kNS - 1) % kNS, min(t + kNS - 1, nk - 1));
+    read_frags(t % kNS);
+    if (grp) wait_vmcnt<kVmWait>();  // Q: k-tile t+1 landed before barrier 2t+2
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    compute();
+    if (!grp) wait_vmcnt<kVmWait>();  // P: k-tile t+1 landed before barrier 2t+2
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (!grp) lds_barrier();
+  // Drain the clamped tail refills before any wave reuses the ring for the
+  // epilogue (and before the workgroup can exit).
+  wait_vmcnt<0>();
+  lds_barrier();
+
+  epilogue_store<OutT>(acc, lds_base + wave * (128 * 64 * 2),
+                       C + (size_t)(m0 + grp * 128) * N + n0 + gw * 64, N, lane);
+}
+
+template <typename OutT>
+hipError_t launch_pp_t(const GemmArgs& a) {
+  static std::atomic<uint64_t> attr_done{0};
+  auto kfn = f16_pp_kernel<OutT>;
+  hipError_t e = ensure_lds_attr(kfn, kLdsBytes, a.device, attr_done);
+  if (e != hipSuccess) return e;
+  const int tiles = (int)((a.m / kBM) * (a.n / kBN));
+  hipLaunchKernelGGL(kfn, dim3(tiles), dim3(kThreads), kLdsBytes, a.stream,
+                     static_cast<const half_t*>(a.A), static_cast<const half_t*>(a.B),
+                     static_cast<OutT*>(a.C), (int)a.m, (int)a.n, (int)a.k);
+  return hipGetLastError();
+}
+
+hipError_t launch_pp(const GemmArgs& a) {
+  return a.out_dtype == VK_DTYPE_F16 ? launch_pp_t<half_t>(a) : launch_pp_t<float>(a);
+}
+
+// 32-bit byte offsets inside one 256-row panel of A and one 32-row slab of B
+// must not overflow; the grid is 1-D.
+bool pp_shape_ok(size_t m, size_t n, size_t k) {
+  return (size_t)kBM * k * 2 < (1ull << 31) && (size_t)kBK * n * 2 < (1ull << 31) &&
+         (m / kBM) * (n / kBN) < (1ull << 31);
+}
+
+}  // namespace
+
+void register_f16_pingpong() {
+  KernelEntry e{};
+  e.version = 5;
+  e.in_dtype = VK_DTYPE_F16;
+  e.name = "f16_v5_pp256_bk32x4";
+  e.caps = make_caps(5, VK_DTYPE_F16, kOutF16 | kOutF32, kBM, kBN, kBK, 16, kBM, kBN, kBK, kThreads,
+                     kLdsBytes, 0, 0);
+  e.launch = launch_pp;
+  e.workspace = nullptr;
+  e.shape_ok = pp_shape_ok;
+  register_kernel(e);
+}
+
+}  // namespace vk

@@ -18,6 +18,7 @@
 //    through the same L2.
 #include "vk_device.hpp"
 #include "vk_internal.hpp"
+#include "vk_tile.hpp"
 
 #include <atomic>
 
@@ -42,28 +43,6 @@ struct SkinnyCfg {
   static_assert(kStages >= 4, "pipeline depth");
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 };
-
-__device__ __forceinline__ uint32_t lds_addr32(const void* p) {
-  return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const char*)p);
-}
-
-#pragma clang diagnostic push
-#pragma clang diagnostic ignored "-Winline-asm"
-// Direct-to-LDS load issued as inline asm (the compiler does not track it and
-// so does not wait on it before unrelated LDS reads); waited for with vmcnt.
-__device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t lds_dst) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
-               :
-               : "s"(lds_dst), "v"(voff), "s"(gbase)
-               : "m0");
-}
-#pragma clang diagnostic pop
-
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
 
 template <int MB, typename OutT>
 __global__ __launch_bounds__(256, 1) void f16_skinny_kernel(const half_t* __restrict__ A,
@@ -148,7 +127,7 @@ __global__ __launch_bounds__(256, 1) void f16_skinny_kernel(const half_t* __rest
     }
     // All reads of this stage must complete before a later iteration's DMA
     // refills it.
-    __builtin_amdgcn_s_waitcnt(0xc07f);  // lgkmcnt(0)
+    wait_lgkmcnt0();
   }
   wait_vmcnt<0>();  // clamped tail refills
 
@@ -184,13 +163,8 @@ hipError_t launch_skinny_t(const GemmArgs& a) {
   using G = SkinnyCfg<MB>;
   static std::atomic<uint64_t> done{0};
   auto kfn = f16_skinny_kernel<MB, OutT>;
-  const uint64_t bit = a.device < 64 ? (1ull << a.device) : 0;
-  if (!bit || !(done.load() & bit)) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kfn),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, G::kLdsBytes);
-    if (e != hipSuccess) return e;
-    done.fetch_or(bit);
-  }
+  hipError_t e = ensure_lds_attr(kfn, G::kLdsBytes, a.device, done);
+  if (e != hipSuccess) return e;
   hipLaunchKernelGGL(kfn, dim3((unsigned)(a.n / kCols)), dim3(256), G::kLdsBytes, a.stream,
                      static_cast<const half_t*>(a.A), static_cast<const half_t*>(a.B),
                      static_cast<OutT*>(a.C), (int)a.m, (int)a.n, (int)a.k);

@@ -65,6 +65,58 @@ __device__ __forceinline__ void global_load_lds16(const void* gptr, void* lds_wa
   __builtin_amdgcn_global_load_lds(gptr, VK_LDS_PTR(void, lds_wave_base), 16, 0, 0);
 }
 
+// 32-bit LDS address of a pointer into workgroup memory.
+__device__ __forceinline__ uint32_t lds_addr32(const void* p) {
+  return (uint32_t)(uintptr_t)((__attribute__((address_space(3))) const char*)p);
+}
+
+__device__ __forceinline__ void lds_write8(uint32_t addr, half4 v) {
+  *reinterpret_cast<__attribute__((address_space(3))) half4*>(addr) = v;
+}
+__device__ __forceinline__ void lds_write16(uint32_t addr, float4v v) {
+  *reinterpret_cast<__attribute__((address_space(3))) float4v*>(addr) = v;
+}
+__device__ __forceinline__ uint4v lds_read16(uint32_t addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) uint4v*>(addr);
+}
+__device__ __forceinline__ half8 lds_read_h8(uint32_t addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) half8*>(addr);
+}
+
+// s_waitcnt with only a vmcnt limit (gfx9 encoding: vmcnt[3:0], expcnt[6:4],
+// lgkmcnt[11:8], vmcnt[5:4] at [15:14]).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+__device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
+
+// Workgroup barrier for LDS producer/consumer hand-off only: waits for this
+// wave's LDS reads (lgkmcnt) but, unlike __syncthreads(), not for its
+// in-flight global->LDS prefetches (vmcnt), which are waited for explicitly.
+// The "memory" clobbers keep the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Direct-to-LDS load: lane l's 16 bytes at gbase + voff land at LDS address
+// lds_dst + 16 * l (lds_dst and gbase are wave-uniform).  Issued as inline
+// asm so the compiler does not track it: it would otherwise treat every later
+// LDS read as aliasing the pending load and wait for all of them (vmcnt(0)),
+// which would drain a prefetch ring.  Completion is awaited explicitly with
+// wait_vmcnt().  Nothing else in these kernels uses M0.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+__device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t lds_dst) {
+  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+               :
+               : "s"(lds_dst), "v"(voff), "s"(gbase)
+               : "m0");
+}
+#pragma clang diagnostic pop
+
 template <typename OutT>
 __device__ __forceinline__ OutT convert_out(float v);
 template <>

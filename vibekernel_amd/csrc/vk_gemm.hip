@@ -34,6 +34,7 @@ void init_registry() {
     register_f16_simple();
     register_f16_dma();
     register_f16_skinny();
+    register_f16_pingpong();
     register_f32_valu();
   });
 }

@@ -47,6 +47,7 @@ void register_kernel(const KernelEntry& e);
 void register_f16_simple();
 void register_f16_dma();
 void register_f16_skinny();
+void register_f16_pingpong();
 void register_f32_valu();
 
 inline vk_caps make_caps(int version, vk_dtype in, int out_mask, uint32_t dm, uint32_t dn,

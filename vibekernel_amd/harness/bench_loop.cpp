@@ -58,3 +58,28 @@ extern "C" int vkb_back_to_back(int version, vk_dtype in_dtype, vk_dtype out_dty
     if (total_ms) *total_ms = ms;
     return VK_OK;
 }
+
+extern "C" int vkb_stream_loop(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, size_t n,
+                               size_t k, const void* A, const void* B, void* C, void* stream, int warmup,
+                               int iters, float* total_ms) {
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    if (iters <= 0) return VK_ERR_SHAPE;
+    for (int i = 0; i < warmup; i++) {
+        int st = vk_gemm(version, in_dtype, out_dtype, m, n, k, A, B, C, stream);
+        if (st != VK_OK) return st;
+    }
+    if (hipDeviceSynchronize() != hipSuccess) return VK_ERR_HIP;
+    Events ev;
+    if (!ev.ok) return VK_ERR_HIP;
+    if (hipEventRecord(ev.a, s) != hipSuccess) return VK_ERR_HIP;
+    for (int i = 0; i < iters; i++) {
+        int st = vk_gemm(version, in_dtype, out_dtype, m, n, k, A, B, C, stream);
+        if (st != VK_OK) return st;
+    }
+    if (hipEventRecord(ev.b, s) != hipSuccess) return VK_ERR_HIP;
+    if (hipEventSynchronize(ev.b) != hipSuccess) return VK_ERR_HIP;
+    float ms = 0.0f;
+    if (hipEventElapsedTime(&ms, ev.a, ev.b) != hipSuccess) return VK_ERR_HIP;
+    if (total_ms) *total_ms = ms;
+    return hipDeviceSynchronize() == hipSuccess ? VK_OK : VK_ERR_HIP;
+}
