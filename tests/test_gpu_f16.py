@@ -125,7 +125,7 @@ def test_rejected_shape_raises_before_launch(gpu):
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("version", [2, 3, 5])
+@pytest.mark.parametrize("version", [2, 3, 5, 6, 7])
 def test_headline_4096_reference_metric(gpu, oracle, version):
     """4096^3 on the reference's own input distribution (N(0,1)) and metric
     (mean relative error of the fp16 C, test_data.hpp:145-162).
@@ -153,7 +153,7 @@ def test_headline_4096_reference_metric(gpu, oracle, version):
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("version", [2, 3, 5])
+@pytest.mark.parametrize("version", [2, 3, 5, 6, 7])
 def test_headline_4096_f32_out(gpu, oracle, version):
     m = n = k = 4096
     A, B = make_inputs(m, n, k, "uniform", seed=7)
@@ -167,7 +167,7 @@ def test_headline_4096_f32_out(gpu, oracle, version):
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("version", [2, 3, 5])
+@pytest.mark.parametrize("version", [2, 3, 5, 6, 7])
 def test_repeat_launch_deterministic(gpu, version):
     """110 launches (the reference caught its cp.async race only after >=110
     runs): C poisoned with NaN before each launch, every result bitwise equal

@@ -8,5 +8,5 @@ from ._abi import DTYPE_F16, DTYPE_F32, VkError, abi_version, lib_path, load  # 
 from .gemm import gemm, matmul, name, pick_version, query, versions  # noqa: F401
 
 # Default fp16 version: the fastest kernel for tile-divisible shapes (256x256 tiles,
-# BK=32, 4-stage direct-to-LDS ring, 8 waves in two phase-shifted groups).
-DEFAULT_F16_VERSION = 5
+# 64-deep k-tiles, 8 waves in two phase-shifted groups, 16x16x32 MFMAs).
+DEFAULT_F16_VERSION = 7

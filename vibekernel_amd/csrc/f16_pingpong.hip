@@ -197,6 +197,7 @@ __global__ __launch_bounds__(kThreads) void f16_pp_kernel(const half_t* __restri
 
   half8 fa[2][4], fb[2][2];
   const int nk = K / kBK;
+  prefer_agpr_accumulators();
 
   auto issue = [&](int stage, int kt) {
     const uint32_t dst = lds_base + stage * kStageBytes + ddst;
@@ -289,6 +290,487 @@ bool pp_shape_ok(size_t m, size_t n, size_t k) {
          (m / kBM) * (n / kBN) < (1ull << 31);
 }
 
+
+// ---------------------------------------------------------------------------
+// Version 6: the same ping-pong with 64-deep k-tiles, so each phase holds 32
+// MFMAs (1024 matrix-core cycles) and the barrier pair costs half as much per
+// FLOP, and with the global->LDS loads moved out of the memory phase.
+//
+// Measured on version 5 and on a first 64-deep variant: a wave that issues its
+// direct-to-LDS loads at the start of its memory phase stalls on them (the
+// texture unit accepts one 1 KB load instruction about every 16 cycles per
+// CU), and its LDS reads queue behind them.  Here the memory phase holds only
+// the LDS fragment reads, and each wave issues its 8 loads of a k-tile during
+// its compute phase, one after every 4 MFMAs, where the wait costs nothing.
+//
+// LDS ring, split by reader (160 KB):
+//    A-top  rows   0..127 of the A k-tile, read by P     2 slots x 16 KB
+//    A-bot  rows 128..255,                   read by Q     2 slots x 16 KB
+//    B      64 x 256,                        read by both  3 slots x 32 KB
+//
+// Phases as in version 5 (P: memory(t) in phase 2t, compute(t) in 2t+1; Q one
+// phase later).  During compute(t):
+//    P loads B(t+2)                 -> B slot (t+2)%3 (B(t-1), read by phase 2t-1)
+//    Q loads A-top(t+2), A-bot(t+2) -> slot t%2 (A-top(t) read in phase 2t,
+//                                      A-bot(t) in phase 2t+1)
+// and the waits that make a k-tile land before the first barrier that opens a
+// phase reading it are:
+//    P after compute(t):  vmcnt(8)  B(t+1)                   (barrier 2t+2)
+//    Q after memory(t):   vmcnt(4)  A-top(t+1)               (barrier 2t+2)
+//    Q after compute(t):  vmcnt(8)  A-top(t+1), A-bot(t+1)   (barrier 2t+3)
+// Refills past the last k-tile are clamped to it and land in slots that are
+// never read again.
+namespace pp64 {
+
+constexpr int kBK = 64;
+constexpr int kHalfBytes = 128 * kBK * 2;  // 16 KB: one A half-tile
+constexpr int kBBytes = kBK * kBN * 2;     // 32 KB
+constexpr int kATop = 0;                   // 2 slots
+constexpr int kABot = 2 * kHalfBytes;      // 2 slots
+constexpr int kBOff = 4 * kHalfBytes;      // 3 slots
+constexpr int kBSlots = 3;
+constexpr int kLdsBytes = kBOff + kBSlots * kBBytes;  // 160 KB
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+static_assert(kLdsBytes >= 8 * 128 * 64 * 2, "fp16 epilogue staging: 16 KB per wave");
+
+template <typename OutT>
+__global__ __launch_bounds__(kThreads) void f16_pp64_kernel(const half_t* __restrict__ A,
+                                                            const half_t* __restrict__ B,
+                                                            OutT* __restrict__ C, int M, int N, int K) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;  // 0 = P, 1 = Q; waves w and w+4 share a SIMD
+  const int gw = wave & 3;
+
+  int tm, tn;
+  tile_of(blockIdx.x, M / kBM, N / kBN, tm, tn);
+  const int m0 = tm * kBM, n0 = tn * kBN;
+  const uint32_t lds_base = lds_addr32(lds);
+
+  // ---- direct-to-LDS duty: 8 instructions (8 KB) per wave per k-tile ----
+  // Instruction d = 4h + i (h = 0, 1; i = 0..3) uses lane offset voff[i]; the
+  // h step and the slot are wave-uniform address terms, so both groups run the
+  // same branch-free code with different scalars.
+  // Q, A: rows gw*32 + 8i .. +7 of the A-top (h = 0) or A-bot (h = 1) half (8
+  //   chunks of 16 B per row), landing at half offset (gw*4 + i) * 1024.
+  // P, B: k-rows gw*16 + 2i + 8h, +1 (32 chunks each), landing at B offset
+  //   (gw*8 + 4h + i) * 1024; +8 k-rows keep the swizzle.
+  uint32_t voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    if (grp) {
+      const int row = gw * 32 + i * 8 + (lane >> 3);
+      const int c = (lane & 7) ^ swz_a<kBK>(row);
+      voff[i] = (uint32_t)(((size_t)row * K + c * 8) * 2);
+    } else {
+      const int krow = gw * 16 + i * 2 + (lane >> 5);
+      const int c = (lane & 31) ^ swz_b(krow);
+      voff[i] = (uint32_t)(((size_t)krow * N + c * 8) * 2);
+    }
+  }
+  const char* a_top = reinterpret_cast<const char*>(A) + (size_t)m0 * K * 2;
+  const char* b_src = reinterpret_cast<const char*>(B) + (size_t)n0 * 2;
+  const char* g_base = grp ? a_top : b_src;
+  const size_t g_kt = grp ? (size_t)kBK * 2 : (size_t)kBK * N * 2;    // per k-tile
+  const size_t g_h = grp ? (size_t)128 * K * 2 : (size_t)8 * N * 2;   // per h
+  const uint32_t l_base = lds_base + (grp ? (uint32_t)kATop + gw * 4 * 1024 : (uint32_t)kBOff + gw * 8 * 1024);
+  const uint32_t l_slot = grp ? (uint32_t)kHalfBytes : (uint32_t)kBBytes;  // per slot
+  const uint32_t l_h = grp ? (uint32_t)(kABot - kATop) : 4096u;           // per h
+
+  // Load instruction d (0..7) of k-tile kt into slot `slot` (P: a B slot, Q:
+  // an A slot).
+  auto dma = [&](int d, int kt, int slot) {
+    const char* g = g_base + (size_t)kt * g_kt + (d >> 2) * g_h;
+    dma16(g, voff[d & 3], l_base + slot * l_slot + (d >> 2) * l_h + (d & 3) * 1024);
+  };
+
+  // ---- fragment addresses ----
+  // A block i, k-step ks: half-row i*32 + lane%32, chunk 2*ks + lane/32.
+  const int arow = lane & 31;
+  const uint32_t a_half = grp ? kABot : kATop;
+  uint32_t aoff[4];
+#pragma unroll
+  for (int ks = 0; ks < 4; ks++)
+    aoff[ks] = a_half + arow * (kBK * 2) + 16 * ((2 * ks + (lane >> 5)) ^ swz_a<kBK>(arow));
+  // B block j, k-step ks, half h: as version 5 (k-row ks*16 + 8*(g/2) + 4h + jj).
+  const int g = lane >> 4, jj = (lane >> 2) & 3, q = lane & 3;
+  uint32_t boff[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int krow0 = 8 * (g >> 1) + jj;
+    const int c = gw * 8 + j * 4 + 2 * (g & 1) + (q >> 1);
+    boff[j] = kBOff + krow0 * (kBN * 2) + 16 * (c ^ swz_b(krow0)) + 8 * (q & 1);
+  }
+
+  float16v acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[i][j][r] = 0.0f;
+
+  half8 fa[4][4], fb[4][2];
+  const int nk = K / kBK;
+  prefer_agpr_accumulators();
+
+  auto read_frags = [&](int aslot, int bslot) {
+    const uint32_t sa = lds_base + aslot * kHalfBytes;
+    const uint32_t sb = lds_base + bslot * kBBytes;
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) fa[ks][i] = lds_read_h8(sa + aoff[ks] + i * 32 * kBK * 2);
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const uint32_t p = sb + boff[j] + ks * 16 * kBN * 2;
+        const half4 lo = lds_read_tr16_at(p);
+        const half4 hi = lds_read_tr16_at(p + 4 * kBN * 2);
+        fb[ks][j] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+    }
+  };
+  // 32 MFMAs with the 8 loads of k-tile kt interleaved, one after every 4.
+  auto compute_and_load = [&](int kt, int slot) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+#pragma unroll
+        for (int j = 0; j < 2; j++) acc[i][j] = mfma32x32x16(fb[ks][j], fa[ks][i], acc[i][j]);
+        if (i & 1) {
+          __builtin_amdgcn_sched_barrier(0);
+          dma(2 * ks + (i >> 1), kt, slot);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+  };
+
+  // Prologue: P loads B(0), B(1); Q loads A-top(0), A-bot(0), A-top(1),
+  // A-bot(1).  Barrier 0 needs A-top(0) and B(0); Q's extra barrier 1 needs
+  // A-bot(0).  The rest is covered by the loop's own waits.
+  const int kt1 = min(1, nk - 1);
+#pragma unroll
+  for (int d = 0; d < 8; d++) dma(d, 0, 0);
+#pragma unroll
+  for (int d = 0; d < 8; d++) dma(d, kt1, 1);
+  if (grp)
+    wait_vmcnt<12>();
+  else
+    wait_vmcnt<8>();
+  lds_barrier();
+  if (grp) {
+    wait_vmcnt<8>();
+    lds_barrier();
+  }
+
+  for (int t = 0; t < nk; t++) {
+    const int aslot = t & 1;
+    const int bslot = t % kBSlots;
+    const int kt2 = min(t + 2, nk - 1);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(aslot, bslot);
+    if (grp) wait_vmcnt<4>();  // Q: A-top(t+1) landed before barrier 2t+2
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    compute_and_load(kt2, grp ? aslot : (t + 2) % kBSlots);
+    wait_vmcnt<8>();  // P: B(t+1); Q: A-top(t+1), A-bot(t+1)
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (!grp) lds_barrier();
+  wait_vmcnt<0>();
+  lds_barrier();
+
+  epilogue_store<OutT>(acc, lds_base + wave * (128 * 64 * 2),
+                       C + (size_t)(m0 + grp * 128) * N + n0 + gw * 64, N, lane);
+}
+
+template <typename OutT>
+hipError_t launch_t(const GemmArgs& a) {
+  static std::atomic<uint64_t> attr_done{0};
+  auto kfn = f16_pp64_kernel<OutT>;
+  hipError_t e = ensure_lds_attr(kfn, kLdsBytes, a.device, attr_done);
+  if (e != hipSuccess) return e;
+  const int tiles = (int)((a.m / kBM) * (a.n / kBN));
+  hipLaunchKernelGGL(kfn, dim3(tiles), dim3(kThreads), kLdsBytes, a.stream,
+                     static_cast<const half_t*>(a.A), static_cast<const half_t*>(a.B),
+                     static_cast<OutT*>(a.C), (int)a.m, (int)a.n, (int)a.k);
+  return hipGetLastError();
+}
+
+hipError_t launch(const GemmArgs& a) {
+  return a.out_dtype == VK_DTYPE_F16 ? launch_t<half_t>(a) : launch_t<float>(a);
+}
+
+// 32-bit lane offsets: 128 rows of A and 64 k-rows of B (the 4-row steps of B
+// and the A-top -> A-bot step are folded into the 64-bit scalar base) must
+// stay below 2^31 bytes.
+bool shape_ok(size_t m, size_t n, size_t k) {
+  return (size_t)128 * k * 2 < (1ull << 31) && (size_t)kBK * n * 2 < (1ull << 31) &&
+         (m / kBM) * (n / kBN) < (1ull << 31);
+}
+
+}  // namespace pp64
+
+// ---------------------------------------------------------------------------
+// Version 7: version 6 with v_mfma_f32_16x16x32_f16 instead of the 32x32x16
+// MFMA.  Same LDS bytes, loads, phases and waits; each wave's 128x64 block is
+// 8x4 blocks of 16x16, 64 MFMAs of 16 cycles per 64-deep k-tile.
+//
+// Why: MI355X runs a sustained GEMM at its power limit, so FLOPs per joule set
+// the clock.  Measured on a pure MFMA stream (random fp16 operands, 2 waves
+// per SIMD, ~97% of issue slots busy): the 16x16x32 form holds ~1.84 GHz where
+// the 32x32x16 form holds ~1.60 GHz.  Per multiply-add the 16x16x32 form moves
+// half the accumulator data (256 outputs per 32-deep instruction instead of
+// 1024 per 16-deep) for twice the operand data, 20% fewer register bytes.
+//
+// Layouts for the 16x16x32 shape (lane l):
+//   A operand (the B fragment here, as in version 5): lane l holds 8
+//     consecutive k of column l % 16, k = 8 * (l / 16) + e;
+//   B operand (the A fragment): 8 consecutive k of row l % 16;
+//   D: lane l, register r holds C^T[4 * (l / 16) + r][l % 16], i.e.
+//     C[row l % 16][column 4 * (l / 16) + r].
+// LDS swizzles, chosen for 16-lane (and 32-lane) access phases:
+//   A rows (128 B = 8 chunks): chunk ^ ((row / 2) % 8): the 16 rows of one
+//     fragment read fill the 16 16-byte slots of the 256-byte bank space;
+//   B k-rows: version 5's chunk ^ {0, 6, 12, 10}[k % 4], additionally ^ 2 for
+//     k-rows with bit 3 set, so the two 16-lane groups of a 32-lane phase
+//     (k-rows 8 apart, same columns) use distinct slots.
+namespace pp16 {
+
+using pp64::kBK;
+using pp64::kHalfBytes;
+using pp64::kBBytes;
+using pp64::kATop;
+using pp64::kABot;
+using pp64::kBOff;
+using pp64::kBSlots;
+using pp64::kLdsBytes;
+
+__host__ __device__ constexpr int swz_a16(int row) { return (row >> 1) & 7; }
+__host__ __device__ constexpr int swz_b16(int krow) { return swz_b(krow) ^ (((krow >> 3) & 1) << 1); }
+
+template <typename OutT>
+__device__ __forceinline__ typename std::enable_if<std::is_same<OutT, half_t>::value>::type
+epilogue16(float4v (&acc)[8][4], uint32_t wbase, OutT* Cw, int N, int lane) {
+  // Block (i, j), register r: C[i*16 + l%16][j*16 + 4*(l/16) + r].
+  const int r0 = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+      const int row = i * 16 + r0;
+      half4 h = {(half_t)acc[i][j][0], (half_t)acc[i][j][1], (half_t)acc[i][j][2], (half_t)acc[i][j][3]};
+      lds_write8(epi16_addr(wbase, row, 2 * j + (g >> 1)) + 8 * (g & 1), h);
+    }
+  const int rsub = lane >> 3, ch = lane & 7;
+#pragma unroll
+  for (int q = 0; q < 16; q++) {
+    const int row = 8 * q + rsub;
+    const uint4v v = lds_read16(epi16_addr(wbase, row, ch));
+    *reinterpret_cast<uint4v*>(Cw + (size_t)row * N + ch * 8) = v;
+  }
+}
+
+template <typename OutT>
+__device__ __forceinline__ typename std::enable_if<std::is_same<OutT, float>::value>::type
+epilogue16(float4v (&acc)[8][4], uint32_t wbase, OutT* Cw, int N, int lane) {
+  const int r0 = lane & 15, g = lane >> 4;
+#pragma unroll
+  for (int pass = 0; pass < 2; pass++) {
+#pragma unroll
+    for (int ii = 0; ii < 4; ii++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const int row = ii * 16 + r0;  // row within this pass
+        const int chunk = 4 * j + g;
+        lds_write16(wbase + row * 256 + 16 * (chunk ^ (row & 15)), acc[4 * pass + ii][j]);
+      }
+    const int rsub = lane >> 4, ch = lane & 15;
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+      const int row = 4 * q + rsub;
+      const uint4v v = lds_read16(wbase + row * 256 + 16 * (ch ^ (row & 15)));
+      *reinterpret_cast<uint4v*>(Cw + (size_t)(pass * 64 + row) * N + ch * 4) = v;
+    }
+    if (pass == 0) wait_lgkmcnt0();  // this wave's region is rewritten by the next pass
+  }
+}
+
+template <typename OutT>
+__global__ __launch_bounds__(kThreads) void f16_pp16_kernel(const half_t* __restrict__ A,
+                                                            const half_t* __restrict__ B,
+                                                            OutT* __restrict__ C, int M, int N, int K) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;  // 0 = P, 1 = Q; waves w and w+4 share a SIMD
+  const int gw = wave & 3;
+
+  int tm, tn;
+  tile_of(blockIdx.x, M / kBM, N / kBN, tm, tn);
+  const int m0 = tm * kBM, n0 = tn * kBN;
+  const uint32_t lds_base = lds_addr32(lds);
+
+  // ---- direct-to-LDS duty: instruction d = 4h + i (8 per wave per k-tile) ----
+  // Q, A: rows gw*32 + 8i .. +7 of the A-top (h = 0) or A-bot (h = 1) half,
+  //   landing at half offset (gw*4 + i) * 1024.
+  // P, B: k-rows gw*16 + 2*(i&1) + 8*(i>>1) + 4h, +1, landing at their own
+  //   row offset (512 B per k-row).  h moves 4 k-rows (bit 2), which the B
+  //   swizzle ignores, so voff[i] serves both h.
+  uint32_t voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    if (grp) {
+      const int row = gw * 32 + i * 8 + (lane >> 3);
+      const int c = (lane & 7) ^ swz_a16(row);
+      voff[i] = (uint32_t)(((size_t)row * K + c * 8) * 2);
+    } else {
+      const int krow = gw * 16 + 2 * (i & 1) + 8 * (i >> 1) + (lane >> 5);
+      const int c = (lane & 31) ^ swz_b16(krow);
+      voff[i] = (uint32_t)(((size_t)krow * N + c * 8) * 2);
+    }
+  }
+  const char* a_top = reinterpret_cast<const char*>(A) + (size_t)m0 * K * 2;
+  const char* b_src = reinterpret_cast<const char*>(B) + (size_t)n0 * 2;
+  const char* g_base = grp ? a_top : b_src;
+  const size_t g_kt = grp ? (size_t)kBK * 2 : (size_t)kBK * N * 2;   // per k-tile
+  const size_t g_h = grp ? (size_t)128 * K * 2 : (size_t)4 * N * 2;  // per h
+  const uint32_t l_base = lds_base + (grp ? (uint32_t)kATop + gw * 4 * 1024 : (uint32_t)kBOff + gw * 16 * 512);
+  const uint32_t l_slot = grp ? (uint32_t)kHalfBytes : (uint32_t)kBBytes;  // per slot
+  const uint32_t l_h = grp ? (uint32_t)(kABot - kATop) : 4u * 512u;       // per h
+
+  auto dma = [&](int d, int kt, int slot) {
+    const int i = d & 3, h = d >> 2;
+    const uint32_t l_i = grp ? (uint32_t)i * 1024 : (uint32_t)((i & 1) * 1024 + (i >> 1) * 4096);
+    const char* gp = g_base + (size_t)kt * g_kt + h * g_h;
+    dma16(gp, voff[i], l_base + slot * l_slot + h * l_h + l_i);
+  };
+
+  // ---- fragment addresses ----
+  // A block i, k-step s: half-row i*16 + l%16, chunk 4s + l/16.
+  const int arow = lane & 15;
+  const uint32_t a_half = grp ? kABot : kATop;
+  uint32_t aoff[2];
+#pragma unroll
+  for (int s2 = 0; s2 < 2; s2++)
+    aoff[s2] = a_half + arow * (kBK * 2) + 16 * ((4 * s2 + (lane >> 4)) ^ swz_a16(arow));
+  // B block j, k-step s, half h: lane 16g + 4jj + q names k-row
+  // 32s + 8g + 4h + jj, columns gw*64 + 16j + 4q .. +3; the transpose read
+  // hands lane 16g + c the 4 k of column 16j + c.
+  const int g = lane >> 4, jj = (lane >> 2) & 3, q = lane & 3;
+  const int krow0 = 8 * g + jj;  // plus 32s + 4h: bits 0, 1, 3 unchanged
+  uint32_t boff[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int c = gw * 8 + 2 * j + (q >> 1);
+    boff[j] = kBOff + krow0 * (kBN * 2) + 16 * (c ^ swz_b16(krow0)) + 8 * (q & 1);
+  }
+
+  float4v acc[8][4];
+#pragma unroll
+  for (int i = 0; i < 8; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+  half8 fa[2][8], fb[2][4];
+  const int nk = K / kBK;
+  prefer_agpr_accumulators();
+
+  auto read_frags = [&](int aslot, int bslot) {
+    const uint32_t sa = lds_base + aslot * kHalfBytes;
+    const uint32_t sb = lds_base + bslot * kBBytes;
+#pragma unroll
+    for (int s2 = 0; s2 < 2; s2++) {
+#pragma unroll
+      for (int i = 0; i < 8; i++) fa[s2][i] = lds_read_h8(sa + aoff[s2] + i * 16 * kBK * 2);
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const uint32_t p = sb + boff[j] + s2 * 32 * kBN * 2;
+        const half4 lo = lds_read_tr16_at(p);
+        const half4 hi = lds_read_tr16_at(p + 4 * kBN * 2);
+        fb[s2][j] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+    }
+  };
+  // 64 MFMAs with the 8 loads of k-tile kt interleaved, one after every 8.
+  auto compute_and_load = [&](int kt, int slot) {
+#pragma unroll
+    for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+#pragma unroll
+        for (int j = 0; j < 4; j++) acc[i][j] = mfma16x16x32(fb[s2][j], fa[s2][i], acc[i][j]);
+        if (i & 1) {
+          __builtin_amdgcn_sched_barrier(0);
+          dma(4 * s2 + (i >> 1), kt, slot);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+  };
+
+  // Prologue and loop: exactly as version 6.
+  const int kt1 = min(1, nk - 1);
+#pragma unroll
+  for (int d = 0; d < 8; d++) dma(d, 0, 0);
+#pragma unroll
+  for (int d = 0; d < 8; d++) dma(d, kt1, 1);
+  if (grp)
+    wait_vmcnt<12>();
+  else
+    wait_vmcnt<8>();
+  lds_barrier();
+  if (grp) {
+    wait_vmcnt<8>();
+    lds_barrier();
+  }
+
+  for (int t = 0; t < nk; t++) {
+    const int aslot = t & 1;
+    const int bslot = t % kBSlots;
+    const int kt2 = min(t + 2, nk - 1);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(aslot, bslot);
+    if (grp) wait_vmcnt<4>();  // Q: A-top(t+1) landed before barrier 2t+2
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    compute_and_load(kt2, grp ? aslot : (t + 2) % kBSlots);
+    wait_vmcnt<8>();  // P: B(t+1); Q: A-top(t+1), A-bot(t+1)
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (!grp) lds_barrier();
+  wait_vmcnt<0>();
+  lds_barrier();
+
+  epilogue16<OutT>(acc, lds_base + wave * (128 * 64 * 2), C + (size_t)(m0 + grp * 128) * N + n0 + gw * 64, N,
+                   lane);
+}
+
+template <typename OutT>
+hipError_t launch_t(const GemmArgs& a) {
+  static std::atomic<uint64_t> attr_done{0};
+  auto kfn = f16_pp16_kernel<OutT>;
+  hipError_t e = ensure_lds_attr(kfn, kLdsBytes, a.device, attr_done);
+  if (e != hipSuccess) return e;
+  const int tiles = (int)((a.m / kBM) * (a.n / kBN));
+  hipLaunchKernelGGL(kfn, dim3(tiles), dim3(kThreads), kLdsBytes, a.stream,
+                     static_cast<const half_t*>(a.A), static_cast<const half_t*>(a.B),
+                     static_cast<OutT*>(a.C), (int)a.m, (int)a.n, (int)a.k);
+  return hipGetLastError();
+}
+
+hipError_t launch(const GemmArgs& a) {
+  return a.out_dtype == VK_DTYPE_F16 ? launch_t<half_t>(a) : launch_t<float>(a);
+}
+
+}  // namespace pp16
 }  // namespace
 
 void register_f16_pingpong() {
@@ -302,6 +784,24 @@ void register_f16_pingpong() {
   e.workspace = nullptr;
   e.shape_ok = pp_shape_ok;
   register_kernel(e);
+
+  KernelEntry e6{};
+  e6.version = 6;
+  e6.in_dtype = VK_DTYPE_F16;
+  e6.name = "f16_v6_pp256_bk64_split";
+  e6.caps = make_caps(6, VK_DTYPE_F16, kOutF16 | kOutF32, kBM, kBN, pp64::kBK, 16, kBM, kBN, pp64::kBK,
+                      kThreads, pp64::kLdsBytes, 0, 0);
+  e6.launch = pp64::launch;
+  e6.workspace = nullptr;
+  e6.shape_ok = pp64::shape_ok;
+  register_kernel(e6);
+
+  KernelEntry e7 = e6;
+  e7.version = 7;
+  e7.name = "f16_v7_pp256_bk64_m16";
+  e7.caps.version = 7;
+  e7.launch = pp16::launch;
+  register_kernel(e7);
 }
 
 }  // namespace vk

@@ -117,6 +117,15 @@ __device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t
 }
 #pragma clang diagnostic pop
 
+// An inline-asm operand in an AGPR marks the kernel as using AGPRs, and the
+// compiler then selects the AGPR form of the MFMAs: accumulators live in the
+// AccVGPR file while LDS fragment loads land in the ordinary VGPRs.  Without it
+// the compiler keeps both in VGPRs (when they fit in 256).
+__device__ __forceinline__ void prefer_agpr_accumulators() {
+  float z = 0.0f;
+  asm volatile("; accumulators in AGPRs %0" ::"a"(z));
+}
+
 template <typename OutT>
 __device__ __forceinline__ OutT convert_out(float v);
 template <>

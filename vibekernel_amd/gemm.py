@@ -96,12 +96,12 @@ def query(version: int, dtype: str = "f16"):
 def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = None) -> int:
     """The fastest version that accepts this shape (checked with vk_gemm_check
     on 4 KiB-aligned placeholder addresses; nothing is launched): for fp16
-    the skinny kernel when M <= 64, then the 256x256 kernels (8-wave first), then the
-    any-shape kernel.  The reference picks versions at build time only
+    the skinny kernel when M <= 64, then the 256x256 kernels (fastest first), then
+    the any-shape kernel.  The reference picks versions at build time only
     (CMakeLists.txt MATMUL_VERSION); this is a convenience of the front end."""
     in_dt = DTYPE_F16 if dtype == "f16" else DTYPE_F32
     out_dt = DTYPE_F16 if (out or dtype) == "f16" else DTYPE_F32
-    order = [4, 5, 3, 2, 1] if in_dt == DTYPE_F16 else [1]
+    order = [4, 7, 6, 5, 3, 2, 1] if in_dt == DTYPE_F16 else [1]
     avail = set(_abi.versions(in_dt))
     for v in order:
         if v in avail and _abi.check(v, in_dt, out_dt, m, n, k, 4096, 4096, 4096) == _abi.VK_OK:
