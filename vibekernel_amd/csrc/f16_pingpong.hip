@@ -749,8 +749,11 @@ __global__ __launch_bounds__(kThreads) void f16_pp16_kernel(const half_t* __rest
   wait_vmcnt<0>();
   lds_barrier();
 
+  // Lane index recomputed from the exec mask, so that no register has to
+  // carry threadIdx.x across the k-loop.
+  const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
   epilogue16<OutT>(acc, lds_base + wave * (128 * 64 * 2), C + (size_t)(m0 + grp * 128) * N + n0 + gw * 64, N,
-                   lane);
+                   lane_e);
 }
 
 template <typename OutT>
