@@ -99,7 +99,8 @@ def test_single_hip_runtime_in_process():
 
 def test_pick_version_follows_shape():
     import vibekernel_amd as vk
-    assert vk.pick_version(16, 8192, 8192) == 4
+    assert vk.pick_version(16, 8192, 8192) == 8
+    assert vk.pick_version(16, 8224, 8192) == 4  # n % 128 != 0: the 32-column kernel
     assert vk.pick_version(4096, 4096, 4096) == 7
     assert vk.pick_version(4096, 4096, 4096, "f16", "f32") == 7
     assert vk.pick_version(4096, 4096, 4128) == 5  # k % 64 != 0: the 32-deep kernel

@@ -233,26 +233,82 @@ def test_mlp_shapes(gpu, oracle, shape):
 
 
 @pytest.mark.slow
-def test_skinny_decode_shape(gpu, oracle):
+@pytest.mark.parametrize("version", [4, 8])
+def test_skinny_decode_shape(gpu, oracle, version):
     """M = 16, N = K = 8192 (the decode-like, HBM-bound configuration) on the
-    skinny kernel, fp16 and fp32 output, against the oracle."""
+    skinny kernels, fp16 and fp32 output, against the oracle."""
     m, n, k = 16, 8192, 8192
     A, B = make_inputs(m, n, k, "uniform", seed=16)
     C64 = oracle.dgemm(A, B)
-    C32 = run_gemm(4, A, B, "f32")
+    C32 = run_gemm(version, A, B, "f32")
     check_f32_out(C32, A, B, C64)
-    C16 = run_gemm(4, A, B, "f16")
+    C16 = run_gemm(version, A, B, "f16")
     check_f16_out(C16, A, B, C64)
     err, st = oracle.mean_rel_err(oracle.hgemm(A, B), C16)
     assert st == oracle.STATUS_OK and err < 2e-4
 
 
-def test_skinny_rejects_wide_m(gpu):
+@pytest.mark.slow
+def test_splitk_skinny_repeat_and_reshape(gpu):
+    """Version 8 splits K over workgroups and reduces through a counter per
+    column block in the library workspace, reset by the last arrival.  110
+    launches must give bitwise-identical C (the last arrival sums the parts in
+    k order), also when calls of other shapes -- a different split count and
+    number of counters -- run in between."""
+    import torch
+    import vibekernel_amd as vk
+    g = torch.Generator(device="cuda:0").manual_seed(8)
+    shapes = [(16, 8192, 8192), (64, 1024, 2048), (32, 384, 96)]
+    data = []
+    for m, n, k in shapes:
+        A = (torch.rand((m, k), generator=g, device="cuda:0") * 2 - 1).half()
+        B = (torch.rand((k, n), generator=g, device="cuda:0") * 2 - 1).half()
+        C = torch.empty((m, n), dtype=torch.float16, device="cuda:0")
+        announce(f"version=8 first call m={m} n={n} k={k}")
+        vk.matmul(m, n, k, A, B, C, 8)
+        data.append((m, n, k, A, B, C, C.clone()))
+    for it in range(110):
+        m, n, k, A, B, C, ref = data[it % len(data)]
+        C.fill_(float("nan"))
+        vk.matmul(m, n, k, A, B, C, 8)
+        assert torch.equal(C, ref), f"call {it}: m={m} n={n} k={k}"
+    torch.cuda.synchronize()
+
+
+def test_splitk_skinny_caller_workspace(gpu, oracle):
+    """vk_gemm_ws with a caller workspace full of garbage: the launch clears the
+    counters it keeps there, so the result equals the library-workspace call."""
+    import torch
+    import vibekernel_amd as vk
+    from vibekernel_amd import _abi
+    m, n, k = 32, 1024, 4096
+    A, B = make_inputs(m, n, k, "uniform", seed=5)
+    ref = run_gemm(8, A, B, "f32")
+    need = _abi.workspace_bytes(8, _abi.DTYPE_F16, m, n, k)
+    assert need > 0
+    ws = torch.full((need // 4 + 64,), -1, dtype=torch.int32, device="cuda:0")
+    tA = torch.from_numpy(A).cuda()
+    tB = torch.from_numpy(B).cuda()
+    for _ in range(3):
+        tC = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+        announce(f"version=8 caller workspace m={m} n={n} k={k}")
+        st = _abi.gemm_ws(8, _abi.DTYPE_F16, _abi.DTYPE_F32, m, n, k, tA.data_ptr(), tB.data_ptr(),
+                          tC.data_ptr(), ws.data_ptr(), ws.numel() * 4)
+        assert st == 0
+        torch.cuda.synchronize()
+        assert np.array_equal(tC.cpu().numpy(), ref)
+    small = _abi.gemm_ws(8, _abi.DTYPE_F16, _abi.DTYPE_F32, m, n, k, tA.data_ptr(), tB.data_ptr(),
+                         tC.data_ptr(), ws.data_ptr(), need - 4)
+    assert small == -6  # VK_ERR_WORKSPACE
+
+
+@pytest.mark.parametrize("version", [4, 8])
+def test_skinny_rejects_wide_m(gpu, version):
     import torch
     import vibekernel_amd as vk
     A = torch.zeros((80, 128), dtype=torch.float16, device="cuda:0")
-    B = torch.zeros((128, 64), dtype=torch.float16, device="cuda:0")
-    C = torch.zeros((80, 64), dtype=torch.float16, device="cuda:0")
+    B = torch.zeros((128, 128), dtype=torch.float16, device="cuda:0")
+    C = torch.zeros((80, 128), dtype=torch.float16, device="cuda:0")
     with pytest.raises(vk.VkError) as e:
-        vk.matmul(80, 64, 128, A, B, C, 4)
+        vk.matmul(80, 128, 128, A, B, C, version)
     assert e.value.status == -3

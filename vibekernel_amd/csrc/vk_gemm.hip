@@ -11,6 +11,7 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <algorithm>
 #include <cstring>
 #include <mutex>
 #include <vector>
@@ -35,6 +36,7 @@ void init_registry() {
     register_f16_dma();
     register_f16_skinny();
     register_f16_pingpong();
+    register_f16_skinny_sk();
     register_f32_valu();
   });
 }
@@ -51,6 +53,7 @@ size_t dtype_size(vk_dtype d) { return d == VK_DTYPE_F16 ? 2 : 4; }
 struct DeviceState {
   void* ws = nullptr;
   size_t ws_bytes = 0;
+  int ws_version = 0;  // version that used the library workspace last (0: none)
   int num_cus = 0;
 };
 std::mutex g_dev_mutex;
@@ -94,6 +97,16 @@ hipError_t zero_output(void* C, size_t count, vk_dtype out, hipStream_t s) {
   return hipGetLastError();
 }
 
+}  // namespace
+
+hipError_t zero_words(void* p, size_t words, hipStream_t s) {
+  const unsigned blocks = (unsigned)std::min<size_t>(1024, (words + 255) / 256);
+  hipLaunchKernelGGL(zero_fill_kernel, dim3(blocks ? blocks : 1), dim3(256), 0, s, (uint32_t*)p, words);
+  return hipGetLastError();
+}
+
+namespace {
+
 int validate(const KernelEntry* e, vk_dtype out, size_t m, size_t n, size_t k, const void* A,
              const void* B, const void* C) {
   if (!e) return VK_ERR_VERSION;
@@ -129,6 +142,7 @@ int run(int version, vk_dtype in, vk_dtype out, size_t m, size_t n, size_t k, co
   if (device_state(dev, &ds) != hipSuccess) return VK_ERR_HIP;
 
   const size_t need = e->workspace ? e->workspace(m, n, k) : 0;
+  bool ws_clean = false;
   if (need > 0) {
     if (library_ws) {
       std::lock_guard<std::mutex> lk(g_dev_mutex);
@@ -140,9 +154,12 @@ int run(int version, vk_dtype in, vk_dtype out, size_t m, size_t n, size_t k, co
         }
         if (hipMalloc(&ds->ws, need) != hipSuccess) return VK_ERR_HIP;
         ds->ws_bytes = need;
+        ds->ws_version = 0;
       }
       ws = ds->ws;
       ws_bytes = ds->ws_bytes;
+      ws_clean = ds->ws_version == version;
+      ds->ws_version = version;
     } else if (!ws || ws_bytes < need) {
       return VK_ERR_WORKSPACE;
     }
@@ -158,6 +175,7 @@ int run(int version, vk_dtype in, vk_dtype out, size_t m, size_t n, size_t k, co
   a.out_dtype = out;
   a.workspace = ws;
   a.workspace_bytes = ws_bytes;
+  a.workspace_clean = ws_clean;
   a.stream = s;
   a.device = dev;
   a.num_cus = ds->num_cus;

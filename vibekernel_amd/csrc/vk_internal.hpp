@@ -21,6 +21,10 @@ struct GemmArgs {
   vk_dtype out_dtype;
   void* workspace;
   size_t workspace_bytes;
+  // True when the workspace is library-managed and was left by the previous
+  // call of this same version (counters it keeps are already reset); false
+  // for a caller workspace or after (re)allocation or use by another version.
+  bool workspace_clean;
   hipStream_t stream;
   int device;
   int num_cus;
@@ -43,11 +47,16 @@ struct KernelEntry {
 
 void register_kernel(const KernelEntry& e);
 
+// Fill `words` 32-bit words with zero on `stream` (a kernel, not
+// hipMemsetAsync, so it may be captured into a graph).
+hipError_t zero_words(void* p, size_t words, hipStream_t stream);
+
 // Per-translation-unit registration hooks (called once from vk_gemm.hip).
 void register_f16_simple();
 void register_f16_dma();
 void register_f16_skinny();
 void register_f16_pingpong();
+void register_f16_skinny_sk();
 void register_f32_valu();
 
 inline vk_caps make_caps(int version, vk_dtype in, int out_mask, uint32_t dm, uint32_t dn,
