@@ -5,15 +5,16 @@
 // and its v0 ground truth (matmul_f32_v0_cblas.cpp:8-12) but no hand-written
 // fp32 kernel; its only GPU fp32 version called cublasSgemm.  This is a
 // register-blocked VALU kernel:
-//   * 128x128 workgroup tile, BK = 16, 256 threads, 8x8 outputs per thread
+//   * 128x128 workgroup tile, BK = 8, 256 threads, 8x8 outputs per thread
 //     held as four 4x4 register blocks (rows ty*4 and 64+ty*4, columns tx*4
 //     and 64+tx*4) so the LDS operand reads are 16-byte and conflict-free;
 //   * A is stored k-major in LDS (transposed on the store) and B as loaded;
 //   * the next k-tile is prefetched from HBM into registers while the current
 //     one is multiplied, then written to the other LDS buffer (one barrier per
 //     k-tile).
-// The build disables packed fp32 (v_pk_fma_f32), so the ceiling is one fp32
-// FMA per lane per clock: half of the 157.3 TFLOP/s figure.
+// The build disables packed fp32 (v_pk_fma_f32); measured, plain v_fmac_f32
+// still exceeds half of the 157.3 TFLOP/s figure (89 TFLOP/s at 4096^3), so
+// that figure is the VALU roofline here.
 #include "vk_device.hpp"
 #include "vk_internal.hpp"
 
@@ -21,8 +22,13 @@ namespace vk {
 namespace {
 
 constexpr int kTile = 128;
-constexpr int kBK = 16;
+// BK = 8: the fully unrolled k-step loop keeps a whole k-tile of operand
+// fragments live (8 k x 16 floats); at BK = 16 that spilled into AGPRs (362
+// registers, 1 wave per SIMD, 290 accvgpr moves per tile) and ran at 50
+// TFLOP/s, at BK = 8 it needs 214 VGPRs, 2 waves per SIMD: 89 TFLOP/s.
+constexpr int kBK = 8;
 constexpr int kApitch = kTile + 4;  // As_t[k][m] row pitch (floats)
+static_assert(kBK == 8 || kBK == 16, "tile load mapping: BK/8 float4 per thread per operand");
 
 template <bool kCheck>
 __global__ __launch_bounds__(256) void f32_valu_kernel(const float* __restrict__ A,
@@ -37,13 +43,15 @@ __global__ __launch_bounds__(256) void f32_valu_kernel(const float* __restrict__
   const int64_t m0 = (int64_t)blockIdx.y * kTile;
   const int64_t n0 = (int64_t)blockIdx.x * kTile;
 
-  // Global load mapping: A: 128 rows x 4 float4 per row; B: 16 rows x 32 float4.
-  float4v ra[2], rb[2];
+  // Global load mapping: A: 128 rows x BK/4 float4 per row; B: BK rows x 32 float4.
+  constexpr int kLd = kBK / 8;  // float4 loads per thread per operand
+  constexpr int kC4 = kBK / 4;  // float4 per A row
+  float4v ra[kLd], rb[kLd];
   auto load_tile = [&](int64_t k0) {
 #pragma unroll
-    for (int e = 0; e < 2; e++) {
+    for (int e = 0; e < kLd; e++) {
       const int idx = tid + 256 * e;
-      const int row = idx >> 2, c4 = idx & 3;
+      const int row = idx / kC4, c4 = idx % kC4;
       const int64_t gr = m0 + row, gc = k0 + c4 * 4;
       if (!kCheck) {
         ra[e] = *reinterpret_cast<const float4v*>(&A[gr * K + gc]);
@@ -54,7 +62,7 @@ __global__ __launch_bounds__(256) void f32_valu_kernel(const float* __restrict__
       }
     }
 #pragma unroll
-    for (int e = 0; e < 2; e++) {
+    for (int e = 0; e < kLd; e++) {
       const int idx = tid + 256 * e;
       const int krow = idx >> 5, c4 = idx & 31;
       const int64_t gr = k0 + krow, gc = n0 + c4 * 4;
@@ -69,14 +77,14 @@ __global__ __launch_bounds__(256) void f32_valu_kernel(const float* __restrict__
   };
   auto store_tile = [&](int buf) {
 #pragma unroll
-    for (int e = 0; e < 2; e++) {
+    for (int e = 0; e < kLd; e++) {
       const int idx = tid + 256 * e;
-      const int row = idx >> 2, c4 = idx & 3;
+      const int row = idx / kC4, c4 = idx % kC4;
 #pragma unroll
       for (int q = 0; q < 4; q++) As[buf][(c4 * 4 + q) * kApitch + row] = ra[e][q];
     }
 #pragma unroll
-    for (int e = 0; e < 2; e++) {
+    for (int e = 0; e < kLd; e++) {
       const int idx = tid + 256 * e;
       const int krow = idx >> 5, c4 = idx & 31;
       *reinterpret_cast<float4v*>(&Bs[buf][krow * kTile + c4 * 4]) = rb[e];

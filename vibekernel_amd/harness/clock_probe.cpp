@@ -7,13 +7,18 @@
 // each window of 200 samples gives the clock over ~4 ms.  Inputs are
 // uniform[-1,1) fp16, as in bench.py.
 //
-// Usage: clock_probe [version] [m] [n] [k] [iters]   (fp16 in, fp16 out)
+// Usage: clock_probe [version] [m] [n] [k] [iters] [f16|f32]   (output dtype = input dtype)
+//
+// The probe wave needs a few VGPRs on one CU: a GEMM whose workgroups use all
+// 512 VGPRs of every SIMD (fp16 versions 6 and 7) is displaced by it and the
+// figures then do not describe the GEMM alone.
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
 #include <cstdio>
 #include <cstdlib>
 #include <random>
+#include <string>
 #include <vector>
 
 #include "playground/utils.hpp"
@@ -43,7 +48,10 @@ int main(int argc, char** argv) {
     const size_t n = argc > 3 ? std::strtoul(argv[3], nullptr, 10) : 4096;
     const size_t k = argc > 4 ? std::strtoul(argv[4], nullptr, 10) : 4096;
     const int iters = argc > 5 ? std::atoi(argv[5]) : 2000;
-    const int st0 = vk_gemm_check(version, VK_DTYPE_F16, VK_DTYPE_F16, m, n, k, (void*)4096, (void*)4096,
+    const bool f32 = argc > 6 && std::string(argv[6]) == "f32";
+    const vk_dtype dt = f32 ? VK_DTYPE_F32 : VK_DTYPE_F16;
+    const size_t es = f32 ? 4 : 2;
+    const int st0 = vk_gemm_check(version, dt, dt, m, n, k, (void*)4096, (void*)4096,
                                   (void*)4096);
     if (st0 != VK_OK || iters < 1) {
         std::fprintf(stderr, "clock_probe: version %d rejects %zux%zux%zu (%s)\n", version, m, n, k,
@@ -51,23 +59,26 @@ int main(int argc, char** argv) {
         return 1;
     }
     std::vector<_Float16> h(std::max(m * k, k * n));
+    std::vector<float> hf(f32 ? h.size() : 0);
     std::mt19937 gen(20261201);
     std::uniform_real_distribution<float> dist(-1.0f, 1.0f);
     for (auto& x : h) x = (_Float16)dist(gen);
+    for (size_t i = 0; i < hf.size(); i++) hf[i] = (float)h[i];
     void *A = nullptr, *B = nullptr, *C = nullptr;
     unsigned long long* d = nullptr;
-    PLAYGROUND_HIP_CHECK(hipMalloc(&A, m * k * 2));
-    PLAYGROUND_HIP_CHECK(hipMalloc(&B, k * n * 2));
-    PLAYGROUND_HIP_CHECK(hipMalloc(&C, m * n * 2));
+    PLAYGROUND_HIP_CHECK(hipMalloc(&A, m * k * es));
+    PLAYGROUND_HIP_CHECK(hipMalloc(&B, k * n * es));
+    PLAYGROUND_HIP_CHECK(hipMalloc(&C, m * n * es));
     PLAYGROUND_HIP_CHECK(hipMalloc(&d, kSamples * 16));
-    PLAYGROUND_HIP_CHECK(hipMemcpy(A, h.data(), m * k * 2, hipMemcpyHostToDevice));
-    PLAYGROUND_HIP_CHECK(hipMemcpy(B, h.data(), k * n * 2, hipMemcpyHostToDevice));
+    const void* src = f32 ? (const void*)hf.data() : (const void*)h.data();
+    PLAYGROUND_HIP_CHECK(hipMemcpy(A, src, m * k * es, hipMemcpyHostToDevice));
+    PLAYGROUND_HIP_CHECK(hipMemcpy(B, src, k * n * es, hipMemcpyHostToDevice));
     hipStream_t s1, s2;
     PLAYGROUND_HIP_CHECK(hipStreamCreate(&s1));
     PLAYGROUND_HIP_CHECK(hipStreamCreate(&s2));
     auto run = [&](int count) {
         for (int i = 0; i < count; i++) {
-            const int st = vk_gemm(version, VK_DTYPE_F16, VK_DTYPE_F16, m, n, k, A, B, C, s1);
+            const int st = vk_gemm(version, dt, dt, m, n, k, A, B, C, s1);
             if (st != VK_OK) {
                 std::fprintf(stderr, "clock_probe: vk_gemm failed: %s\n", vk_status_string(st));
                 std::exit(1);
@@ -90,7 +101,7 @@ int main(int argc, char** argv) {
     std::vector<unsigned long long> o(2 * kSamples);
     PLAYGROUND_HIP_CHECK(hipMemcpy(o.data(), d, kSamples * 16, hipMemcpyDeviceToHost));
     const double per = ms / iters;
-    std::printf("%s %zux%zux%zu: %d launches back to back, %.4f ms each, %.1f TFLOPS\n", vk_gemm_name(version, VK_DTYPE_F16), m,
+    std::printf("%s %zux%zux%zu: %d launches back to back, %.4f ms each, %.1f TFLOPS\n", vk_gemm_name(version, dt), m,
                 n, k, iters, per, 2.0 * m * n * k / per / 1e9);
     std::printf("probe: %d samples over %.0f us (GEMM run: %.0f us)\n", kSamples,
                 (o[2 * (kSamples - 1) + 1] - o[1]) / 100.0, ms * 1e3);
