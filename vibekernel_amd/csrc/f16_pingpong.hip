@@ -681,21 +681,30 @@ __global__ __launch_bounds__(kThreads) void f16_pp16_kernel(const half_t* __rest
   const int nk = K / kBK;
   prefer_agpr_accumulators();
 
+  // One per-lane base address per A k-step and per B block (6 VALU adds per
+  // phase); the block, k-step and half offsets (< 64 KB) go into the reads'
+  // immediate offset fields.
   auto read_frags = [&](int aslot, int bslot) {
     const uint32_t sa = lds_base + aslot * kHalfBytes;
     const uint32_t sb = lds_base + bslot * kBBytes;
+    uint32_t va[2], vb[4];
 #pragma unroll
-    for (int s2 = 0; s2 < 2; s2++) {
+    for (int s2 = 0; s2 < 2; s2++) va[s2] = sa + aoff[s2];
 #pragma unroll
-      for (int i = 0; i < 8; i++) fa[s2][i] = lds_read_h8(sa + aoff[s2] + i * 16 * kBK * 2);
+    for (int j = 0; j < 4; j++) vb[j] = sb + boff[j];
+    static_for<2>([&](auto s2c) {
+      constexpr int s2 = decltype(s2c)::value;
+      static_for<8>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        fa[s2][i] = lds_read_h8_off<i * 16 * kBK * 2>(va[s2]);
+      });
 #pragma unroll
       for (int j = 0; j < 4; j++) {
-        const uint32_t p = sb + boff[j] + s2 * 32 * kBN * 2;
-        const half4 lo = lds_read_tr16_at(p);
-        const half4 hi = lds_read_tr16_at(p + 4 * kBN * 2);
+        const half4 lo = lds_read_tr16_off<s2 * 32 * kBN * 2>(vb[j]);
+        const half4 hi = lds_read_tr16_off<s2 * 32 * kBN * 2 + 4 * kBN * 2>(vb[j]);
         fb[s2][j] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
-    }
+    });
   };
   // 64 MFMAs with the 8 loads of k-tile kt interleaved, one after every 8.
   auto compute_and_load = [&](int kt, int slot) {

@@ -26,6 +26,8 @@
 #include <hip/hip_runtime.h>
 
 #include <cstdint>
+#include <type_traits>
+#include <utility>
 
 namespace vk {
 
@@ -81,6 +83,39 @@ __device__ __forceinline__ uint4v lds_read16(uint32_t addr) {
 }
 __device__ __forceinline__ half8 lds_read_h8(uint32_t addr) {
   return *reinterpret_cast<const __attribute__((address_space(3))) half8*>(addr);
+}
+
+// LDS reads at base + OFF with OFF in the instruction's 16-bit offset field
+// (inline asm: the compiler otherwise materialises base + OFF with a VALU add
+// per read).  The "memory" clobber-free asm is ordered by its data use only;
+// callers wait with lgkmcnt (or a barrier) before the results are used.
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
+template <int OFF>
+__device__ __forceinline__ half8 lds_read_h8_off(uint32_t base) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  half8 v;
+  asm volatile("ds_read_b128 %0, %1 offset:%2" : "=v"(v) : "v"(base), "n"(OFF));
+  return v;
+}
+template <int OFF>
+__device__ __forceinline__ half4 lds_read_tr16_off(uint32_t base) {
+  static_assert(OFF >= 0 && OFF < 65536, "ds offset field");
+  half4 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(base), "n"(OFF));
+  return v;
+}
+#pragma clang diagnostic pop
+
+// Calls f(std::integral_constant<int, I>) for I = 0 .. N-1 (compile-time loop
+// indices for template arguments such as immediate offsets).
+template <typename F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+  (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
 }
 
 // s_waitcnt with only a vmcnt limit (gfx9 encoding: vmcnt[3:0], expcnt[6:4],
