@@ -89,6 +89,21 @@ def test_workspace_bytes_zero_for_plain_versions():
             assert _abi.workspace_bytes(v, _abi.DTYPE_F16, 4096, 4096, 4096) == 0
 
 
+def test_splittail_workspace_follows_schedule():
+    """Version 9 needs a workspace only where its schedule splits tiles: the
+    8 KB counter block plus one 256 KB partial slot per split-tail unit (no
+    device here: an MI355X's 256 CUs are assumed)."""
+    from vibekernel_amd import _abi
+    f16 = _abi.DTYPE_F16
+    assert _abi.query(9, f16).uses_workspace == 1
+    assert _abi.workspace_bytes(9, f16, 4096, 4096, 4096) == 0     # one full wave
+    assert _abi.workspace_bytes(9, f16, 4096, 11008, 4096) == 0    # tail of 176 tiles: left whole
+    assert _abi.workspace_bytes(9, f16, 2048, 2048, 4096) == 8192 + 256 * 256 * 1024  # 64 tiles x 4 pieces
+    assert _abi.workspace_bytes(9, f16, 768, 2560, 4096) == 8192 + 120 * 256 * 1024   # 30 tiles x 4 pieces
+    assert _abi.workspace_bytes(9, f16, 2560, 2560, 2048) == 0     # 100 tiles of 32 k-tiles: no gain modelled
+    assert _abi.workspace_bytes(9, f16, 256, 256, 512) == 0        # 8 k-tiles: too shallow to split
+
+
 def test_single_hip_runtime_in_process():
     """The library must bind to the HIP runtime the process already uses
     (PyTorch's), never map a second one."""
@@ -101,8 +116,11 @@ def test_pick_version_follows_shape():
     import vibekernel_amd as vk
     assert vk.pick_version(16, 8192, 8192) == 8
     assert vk.pick_version(16, 8224, 8192) == 4  # n % 128 != 0: the 32-column kernel
-    assert vk.pick_version(4096, 4096, 4096) == 7
+    assert vk.pick_version(4096, 4096, 4096) == 7  # 256 tiles: one full wave
     assert vk.pick_version(4096, 4096, 4096, "f16", "f32") == 7
+    assert vk.pick_version(4096, 11008, 4096) == 7  # 688 tiles = 2.69 waves: tail left whole
+    assert vk.pick_version(2048, 2048, 4096) == 9   # 64 tiles: split k
+    assert vk.pick_version(3840, 4096, 4096) == 7   # 240 of 256 CUs busy: not worth a split
     assert vk.pick_version(4096, 4096, 4128) == 5  # k % 64 != 0: the 32-deep kernel
     assert vk.pick_version(100, 300, 70) == 1
     assert vk.pick_version(512, 512, 512, "f32") == 1

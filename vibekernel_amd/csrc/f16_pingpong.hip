@@ -35,8 +35,10 @@
 // Both groups pass the same number of barriers: 1 + 1 + 2 nk + 1.
 #include "vk_device.hpp"
 #include "vk_internal.hpp"
+#include "vk_streamk.hpp"
 #include "vk_tile.hpp"
 
+#include <algorithm>
 #include <atomic>
 #include <type_traits>
 
@@ -554,68 +556,74 @@ using pp64::kLdsBytes;
 __host__ __device__ constexpr int swz_a16(int row) { return (row >> 1) & 7; }
 __host__ __device__ constexpr int swz_b16(int krow) { return swz_b(krow) ^ (((krow >> 3) & 1) << 1); }
 
+// Store of a wave's 128x64 block of C through its 16 KB LDS staging region,
+// in two halves of 64 rows: stage() the 16 MFMA blocks (i, j) of a half, then
+// flush() it.  Block (i, j), register r, lane l holds
+// C[i*16 + l%16][j*16 + 4*(l/16) + r].
 template <typename OutT>
-__device__ __forceinline__ typename std::enable_if<std::is_same<OutT, half_t>::value>::type
-epilogue16(float4v (&acc)[8][4], uint32_t wbase, OutT* Cw, int N, int lane) {
-  // Block (i, j), register r: C[i*16 + l%16][j*16 + 4*(l/16) + r].
-  const int r0 = lane & 15, g = lane >> 4;
-#pragma unroll
-  for (int i = 0; i < 8; i++)
-#pragma unroll
-    for (int j = 0; j < 4; j++) {
-      const int row = i * 16 + r0;
-      half4 h = {(half_t)acc[i][j][0], (half_t)acc[i][j][1], (half_t)acc[i][j][2], (half_t)acc[i][j][3]};
-      lds_write8(epi16_addr(wbase, row, 2 * j + (g >> 1)) + 8 * (g & 1), h);
-    }
-  const int rsub = lane >> 3, ch = lane & 7;
-#pragma unroll
-  for (int q = 0; q < 16; q++) {
-    const int row = 8 * q + rsub;
-    const uint4v v = lds_read16(epi16_addr(wbase, row, ch));
-    *reinterpret_cast<uint4v*>(Cw + (size_t)row * N + ch * 8) = v;
-  }
-}
+struct Epi16;
 
-template <typename OutT>
-__device__ __forceinline__ typename std::enable_if<std::is_same<OutT, float>::value>::type
-epilogue16(float4v (&acc)[8][4], uint32_t wbase, OutT* Cw, int N, int lane) {
-  const int r0 = lane & 15, g = lane >> 4;
+// fp16: the whole 128x64 block fits the region (row pitch 128 B, see
+// epi16_addr), so only the second flush() stores, 8 rows x 8 chunks per read.
+template <>
+struct Epi16<half_t> {
+  static __device__ __forceinline__ void stage(uint32_t wbase, int lane, int i, int j, const float4v& v) {
+    const int r0 = lane & 15, g = lane >> 4;
+    half4 h = {(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+    lds_write8(epi16_addr(wbase, i * 16 + r0, 2 * j + (g >> 1)) + 8 * (g & 1), h);
+  }
+  static __device__ __forceinline__ void flush(uint32_t wbase, half_t* Cw, int N, int lane, int half) {
+    if (half == 0) return;
+    const int rsub = lane >> 3, ch = lane & 7;
 #pragma unroll
-  for (int pass = 0; pass < 2; pass++) {
-#pragma unroll
-    for (int ii = 0; ii < 4; ii++)
-#pragma unroll
-      for (int j = 0; j < 4; j++) {
-        const int row = ii * 16 + r0;  // row within this pass
-        const int chunk = 4 * j + g;
-        lds_write16(wbase + row * 256 + 16 * (chunk ^ (row & 15)), acc[4 * pass + ii][j]);
-      }
+    for (int q = 0; q < 16; q++) {
+      const int row = 8 * q + rsub;
+      const uint4v v = lds_read16(epi16_addr(wbase, row, ch));
+      *reinterpret_cast<uint4v*>(Cw + (size_t)row * N + ch * 8) = v;
+    }
+  }
+};
+
+// fp32: 64 rows per half (row pitch 256 B = 16 chunks, physical chunk =
+// chunk ^ (row % 16)), 4 rows per read.
+template <>
+struct Epi16<float> {
+  static __device__ __forceinline__ void stage(uint32_t wbase, int lane, int i, int j, const float4v& v) {
+    const int row = (i & 3) * 16 + (lane & 15);  // row within the half
+    const int chunk = 4 * j + (lane >> 4);
+    lds_write16(wbase + row * 256 + 16 * (chunk ^ (row & 15)), v);
+  }
+  static __device__ __forceinline__ void flush(uint32_t wbase, float* Cw, int N, int lane, int half) {
     const int rsub = lane >> 4, ch = lane & 15;
 #pragma unroll
     for (int q = 0; q < 16; q++) {
       const int row = 4 * q + rsub;
       const uint4v v = lds_read16(wbase + row * 256 + 16 * (ch ^ (row & 15)));
-      *reinterpret_cast<uint4v*>(Cw + (size_t)(pass * 64 + row) * N + ch * 4) = v;
+      *reinterpret_cast<uint4v*>(Cw + (size_t)(half * 64 + row) * N + ch * 4) = v;
     }
-    if (pass == 0) wait_lgkmcnt0();  // this wave's region is rewritten by the next pass
+    if (half == 0) wait_lgkmcnt0();  // the region is rewritten by the second half
+  }
+};
+
+template <typename OutT>
+__device__ __forceinline__ void epilogue16(float4v (&acc)[8][4], uint32_t wbase, OutT* Cw, int N, int lane) {
+#pragma unroll
+  for (int half = 0; half < 2; half++) {
+#pragma unroll
+    for (int i = 4 * half; i < 4 * half + 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) Epi16<OutT>::stage(wbase, lane, i, j, acc[i][j]);
+    Epi16<OutT>::flush(wbase, Cw, N, lane, half);
   }
 }
 
-template <typename OutT>
-__global__ __launch_bounds__(kThreads) void f16_pp16_kernel(const half_t* __restrict__ A,
-                                                            const half_t* __restrict__ B,
-                                                            OutT* __restrict__ C, int M, int N, int K) {
-  extern __shared__ __attribute__((aligned(1024))) char lds[];
-  const int lane = threadIdx.x & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int grp = wave >> 2;  // 0 = P, 1 = Q; waves w and w+4 share a SIMD
-  const int gw = wave & 3;
-
-  int tm, tn;
-  tile_of(blockIdx.x, M / kBM, N / kBN, tm, tn);
-  const int m0 = tm * kBM, n0 = tn * kBN;
-  const uint32_t lds_base = lds_addr32(lds);
-
+// The k-loop of one 256x256 tile over k-tiles kb .. kb + nk - 1 (nk >= 1):
+// zeroes `acc`, runs the prologue, the two-phase loop and the closing
+// barriers, and leaves the wave's 128x64 block of C in `acc` with the LDS ring
+// idle.  A and B point at the whole matrices; m0, n0 name the tile.
+__device__ __forceinline__ void pp16_mainloop(const half_t* __restrict__ A, const half_t* __restrict__ B, int N,
+                                              int K, int m0, int n0, int kb, int nk, uint32_t lds_base, int grp,
+                                              int gw, int lane, float4v (&acc)[8][4]) {
   // ---- direct-to-LDS duty: instruction d = 4h + i (8 per wave per k-tile) ----
   // Q, A: rows gw*32 + 8i .. +7 of the A-top (h = 0) or A-bot (h = 1) half,
   //   landing at half offset (gw*4 + i) * 1024.
@@ -635,8 +643,8 @@ __global__ __launch_bounds__(kThreads) void f16_pp16_kernel(const half_t* __rest
       voff[i] = (uint32_t)(((size_t)krow * N + c * 8) * 2);
     }
   }
-  const char* a_top = reinterpret_cast<const char*>(A) + (size_t)m0 * K * 2;
-  const char* b_src = reinterpret_cast<const char*>(B) + (size_t)n0 * 2;
+  const char* a_top = reinterpret_cast<const char*>(A) + ((size_t)m0 * K + (size_t)kb * kBK) * 2;
+  const char* b_src = reinterpret_cast<const char*>(B) + ((size_t)kb * kBK * N + n0) * 2;
   const char* g_base = grp ? a_top : b_src;
   const size_t g_kt = grp ? (size_t)kBK * 2 : (size_t)kBK * N * 2;   // per k-tile
   const size_t g_h = grp ? (size_t)128 * K * 2 : (size_t)4 * N * 2;  // per h
@@ -671,14 +679,12 @@ __global__ __launch_bounds__(kThreads) void f16_pp16_kernel(const half_t* __rest
     boff[j] = kBOff + krow0 * (kBN * 2) + 16 * (c ^ swz_b16(krow0)) + 8 * (q & 1);
   }
 
-  float4v acc[8][4];
 #pragma unroll
   for (int i = 0; i < 8; i++)
 #pragma unroll
     for (int j = 0; j < 4; j++) acc[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
 
   half8 fa[2][8], fb[2][4];
-  const int nk = K / kBK;
   prefer_agpr_accumulators();
 
   // One per-lane base address per A k-step and per B block (6 VALU adds per
@@ -757,12 +763,33 @@ __global__ __launch_bounds__(kThreads) void f16_pp16_kernel(const half_t* __rest
   if (!grp) lds_barrier();
   wait_vmcnt<0>();
   lds_barrier();
+}
 
-  // Lane index recomputed from the exec mask, so that no register has to
-  // carry threadIdx.x across the k-loop.
-  const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+// Lane index recomputed from the exec mask, so that no register has to carry
+// threadIdx.x across the k-loop.
+__device__ __forceinline__ int lane_from_exec() {
+  return (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+}
+
+template <typename OutT>
+__global__ __launch_bounds__(kThreads) void f16_pp16_kernel(const half_t* __restrict__ A,
+                                                            const half_t* __restrict__ B,
+                                                            OutT* __restrict__ C, int M, int N, int K) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;  // 0 = P, 1 = Q; waves w and w+4 share a SIMD
+  const int gw = wave & 3;
+
+  int tm, tn;
+  tile_of(blockIdx.x, M / kBM, N / kBN, tm, tn);
+  const int m0 = tm * kBM, n0 = tn * kBN;
+  const uint32_t lds_base = lds_addr32(lds);
+
+  float4v acc[8][4];
+  pp16_mainloop(A, B, N, K, m0, n0, 0, K / kBK, lds_base, grp, gw, lane, acc);
   epilogue16<OutT>(acc, lds_base + wave * (128 * 64 * 2), C + (size_t)(m0 + grp * 128) * N + n0 + gw * 64, N,
-                   lane_e);
+                   lane_from_exec());
 }
 
 template <typename OutT>
@@ -780,6 +807,171 @@ hipError_t launch_t(const GemmArgs& a) {
 
 hipError_t launch(const GemmArgs& a) {
   return a.out_dtype == VK_DTYPE_F16 ? launch_t<half_t>(a) : launch_t<float>(a);
+}
+
+// ---------------------------------------------------------------------------
+// Version 9: version 7's tile loop with a split tail, for grids whose last
+// wave of 256x256 tiles would leave compute units idle (the reference's
+// answer to the same problem is stream-K, results/naive_fable_cycle2/src/
+// matmul_f16/matmul_f16_v9_streamk.cu:383-448, and the tail lesson of
+// matmul_f16_v42_shfl2.cu:182-189).  The schedule (vk_streamk.hpp): whole
+// tiles first, in version 7's order, then each tail tile cut into s aligned
+// k-slices computed by s workgroups at once.  The pieces of a split tile are
+// summed by whichever of them finishes last:
+//  * each wave handles its own 128x64 block of the tile on its own, with one
+//    arrival counter per (tile, wave), so the hand-off needs no workgroup
+//    barrier;
+//  * a finishing wave first reads the counter: if every other piece has
+//    already arrived it is the last and skips writing its partial; otherwise
+//    it writes its fp32 partial (stores that do not stay dirty in the XCD's
+//    L2), waits for them to complete, and increments the counter; the one that
+//    sees count == pieces - 1 is the last;
+//  * the last one sums the pieces in k order, P0 + P1 + ..., its own piece
+//    taken from registers, so the result does not depend on arrival order,
+//    stores C and resets the counter to 0 for the next call.
+// When the schedule splits nothing every tile runs whole, as version 7.
+constexpr size_t kSkSlotBytes = (size_t)kBM * kBN * sizeof(float);  // one tile's fp32 partial
+
+size_t sk_workspace(size_t m, size_t n, size_t k, int num_cus) {
+  const SkPlan p = sk_plan((int64_t)((m / kBM) * (n / kBN)), (int64_t)(k / kBK), num_cus);
+  return p.units ? kSkCounterBytes + (size_t)p.units * kSkSlotBytes : 0;
+}
+
+// Partial slots are read and written through a buffer resource with the sc1
+// cache policy (the encoding of agent-scope atomic loads and stores): such
+// stores do not stay dirty in the writing XCD's L2, and such loads are not
+// served stale from the reading XCD's L2.
+constexpr int kCpolAgent = 16;  // sc1
+__device__ __forceinline__ void store_partial(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float4v v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uint4v, v), r, voff, soff, kCpolAgent);
+}
+__device__ __forceinline__ float4v load_partial(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kCpolAgent));
+}
+
+// Hand-off of one wave's block of a tile split into np pieces; this wave holds
+// piece p.  part_off(q) is the byte offset of the wave's region of piece q's
+// partial slot: 32 blocks (i, j) x 64 lanes x 16 bytes, so every access is a
+// 1 KB coalesced row.  Returns whether this wave is the last to arrive.
+template <typename PartOff>
+__device__ __forceinline__ bool sk_arrive(float4v (&acc)[8][4], int np, int p, __amdgpu_buffer_rsrc_t part,
+                                          PartOff part_off, unsigned* cnt) {
+  const int lane = lane_from_exec();
+  const unsigned seen =
+      __builtin_amdgcn_readfirstlane(__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  if (seen == (unsigned)(np - 1)) return true;  // every other piece is in memory
+  const uint32_t soff = part_off(p);
+#pragma unroll
+  for (int b = 0; b < 32; b++) store_partial(part, (uint32_t)lane * 16 + b * 1024, soff, acc[b >> 2][b & 3]);
+  wait_vmcnt<0>();  // the partial is in memory before the counter moves
+  unsigned old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __builtin_amdgcn_readfirstlane(old) == (unsigned)(np - 1);
+}
+
+// Store of the wave's block of C: acc alone for a whole tile (np = 1); for a
+// split tile, the last arrival's sum of all pieces, after which the counter is
+// reset for the next call.
+template <typename OutT, typename PartOff>
+__device__ __forceinline__ void sk_write_c(float4v (&acc)[8][4], int np, int p, __amdgpu_buffer_rsrc_t part,
+                                           PartOff part_off, unsigned* cnt, uint32_t wstage, OutT* Cw, int N) {
+  const int lane = lane_from_exec();
+  const uint32_t vlane = (uint32_t)lane * 16;
+  // C = P0 + P1 + ... + P(np-1), left to right, with P(p) = acc, summed 8
+  // blocks at a time (the 8 loads of a piece issued together) and staged for
+  // the store as each batch completes.
+#pragma unroll
+  for (int half = 0; half < 2; half++) {
+#pragma unroll
+    for (int bb = 2 * half; bb < 2 * half + 2; bb++) {
+      float4v t[8], x[8];
+      for (int q = 0; q < p; q++) {
+        const uint32_t soff = part_off(q);
+#pragma unroll
+        for (int b = 0; b < 8; b++) x[b] = load_partial(part, vlane + (8 * bb + b) * 1024, soff);
+#pragma unroll
+        for (int b = 0; b < 8; b++) t[b] = q == 0 ? x[b] : t[b] + x[b];
+      }
+#pragma unroll
+      for (int b = 0; b < 8; b++) t[b] = p == 0 ? acc[2 * bb + (b >> 2)][b & 3] : t[b] + acc[2 * bb + (b >> 2)][b & 3];
+      for (int q = p + 1; q < np; q++) {
+        const uint32_t soff = part_off(q);
+#pragma unroll
+        for (int b = 0; b < 8; b++) x[b] = load_partial(part, vlane + (8 * bb + b) * 1024, soff);
+#pragma unroll
+        for (int b = 0; b < 8; b++) t[b] += x[b];
+      }
+#pragma unroll
+      for (int b = 0; b < 8; b++) Epi16<OutT>::stage(wstage, lane, 2 * bb + (b >> 2), b & 3, t[b]);
+    }
+    Epi16<OutT>::flush(wstage, Cw, N, lane, half);
+  }
+  if (np > 1 && lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+template <typename OutT>
+__global__ __launch_bounds__(kThreads) void f16_pp16_sk_kernel(const half_t* __restrict__ A,
+                                                               const half_t* __restrict__ B,
+                                                               OutT* __restrict__ C, int M, int N, int K, int dp,
+                                                               int units, int pieces, int chunks,
+                                                               float* __restrict__ part,
+                                                               unsigned* __restrict__ counters) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;
+  const int gw = wave & 3;
+  const int tiles_m = M / kBM, tiles_n = N / kBN, T = tiles_m * tiles_n;
+  const int I = K / kBK;
+  const uint32_t lds_base = lds_addr32(lds);
+  const uint32_t wstage = lds_base + wave * (128 * 64 * 2);
+  const int bid = blockIdx.x;
+
+  const SkPlan plan{dp, units, pieces, chunks};
+  const SkWork w = sk_work(bid, T, I, plan);
+  int tm, tn;
+  raster_tile(w.cid, tiles_m, tiles_n, tm, tn);
+  const int m0 = tm * kBM, n0 = tn * kBN;
+  float4v acc[8][4];
+  pp16_mainloop(A, B, N, K, m0, n0, w.kb, w.ke - w.kb, lds_base, grp, gw, lane, acc);
+  OutT* Cw = C + (size_t)(m0 + grp * 128) * N + n0 + gw * 64;
+  // One partial slot per split-tail unit (at most 256: 64 MB, within 32-bit
+  // offsets); piece q of this tile is in the slot of unit sk_unit_of(.., q).
+  const __amdgpu_buffer_rsrc_t prsrc =
+      __builtin_amdgcn_make_buffer_rsrc(part, 0, (int)(units * kSkSlotBytes), kBufferWord3);
+  auto part_off = [&](int q) {
+    return (uint32_t)(sk_unit_of(plan, T, w.tile, q) * kSkSlotBytes) + (uint32_t)wave * (128 * 64 * 4);
+  };
+  unsigned* cnt = counters + (size_t)w.tile * kSkWaves + wave;
+  if (w.np == 1 || sk_arrive(acc, w.np, w.p, prsrc, part_off, cnt))
+    sk_write_c<OutT>(acc, w.np, w.p, prsrc, part_off, cnt, wstage, Cw, N);
+}
+
+template <typename OutT>
+hipError_t launch_sk_t(const GemmArgs& a) {
+  static std::atomic<uint64_t> attr_done{0};
+  auto kfn = f16_pp16_sk_kernel<OutT>;
+  hipError_t e = ensure_lds_attr(kfn, kLdsBytes, a.device, attr_done);
+  if (e != hipSuccess) return e;
+  const SkPlan p = sk_plan((int64_t)((a.m / kBM) * (a.n / kBN)), (int64_t)(a.k / kBK), a.num_cus);
+  unsigned* counters = nullptr;
+  float* part = nullptr;
+  if (p.units > 0) {
+    counters = static_cast<unsigned*>(a.workspace);
+    part = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + kSkCounterBytes);
+    if (!a.workspace_clean) {
+      e = zero_words(counters, kSkCounterBytes / sizeof(unsigned), a.stream);
+      if (e != hipSuccess) return e;
+    }
+  }
+  hipLaunchKernelGGL(kfn, dim3((unsigned)(p.dp + p.units)), dim3(kThreads), kLdsBytes, a.stream,
+                     static_cast<const half_t*>(a.A), static_cast<const half_t*>(a.B), static_cast<OutT*>(a.C),
+                     (int)a.m, (int)a.n, (int)a.k, p.dp, p.units, p.pieces, p.chunks, part, counters);
+  return hipGetLastError();
+}
+
+hipError_t launch_sk(const GemmArgs& a) {
+  return a.out_dtype == VK_DTYPE_F16 ? launch_sk_t<half_t>(a) : launch_sk_t<float>(a);
 }
 
 }  // namespace pp16
@@ -814,6 +1006,15 @@ void register_f16_pingpong() {
   e7.caps.version = 7;
   e7.launch = pp16::launch;
   register_kernel(e7);
+
+  KernelEntry e9 = e7;
+  e9.version = 9;
+  e9.name = "f16_v9_pp256_streamk";
+  e9.caps.version = 9;
+  e9.caps.uses_workspace = 1;
+  e9.launch = pp16::launch_sk;
+  e9.workspace = pp16::sk_workspace;
+  register_kernel(e9);
 }
 
 }  // namespace vk

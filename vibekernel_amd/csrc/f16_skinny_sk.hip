@@ -263,7 +263,7 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
 
 size_t sk_counter_bytes(size_t n) { return ((n / 128) * sizeof(unsigned) + 255) & ~(size_t)255; }
 
-size_t sk_workspace(size_t m, size_t n, size_t k) {
+size_t sk_workspace(size_t m, size_t n, size_t k, int) {
   const int mb = (int)((m + 15) / 16);
   return sk_counter_bytes(n) + (size_t)pick_ks(n, k) * n * 16 * mb * sizeof(float);
 }

@@ -39,6 +39,10 @@ typedef float float16v __attribute__((ext_vector_type(16)));
 typedef float float4v __attribute__((ext_vector_type(4)));
 typedef uint32_t uint4v __attribute__((ext_vector_type(4)));
 
+// Word 3 of a raw (unstrided, byte-addressed) buffer resource on gfx9-family
+// GPUs: data format 32-bit, everything else zero.
+constexpr int kBufferWord3 = 0x00020000;
+
 #define VK_LDS_PTR(T, p) ((__attribute__((address_space(3))) T*)(p))
 
 __device__ __forceinline__ float16v mfma32x32x16(const half8& a, const half8& b, const float16v& c) {

@@ -141,7 +141,7 @@ int run(int version, vk_dtype in, vk_dtype out, size_t m, size_t n, size_t k, co
   DeviceState* ds = nullptr;
   if (device_state(dev, &ds) != hipSuccess) return VK_ERR_HIP;
 
-  const size_t need = e->workspace ? e->workspace(m, n, k) : 0;
+  const size_t need = e->workspace ? e->workspace(m, n, k, ds->num_cus) : 0;
   bool ws_clean = false;
   if (need > 0) {
     if (library_ws) {
@@ -205,7 +205,12 @@ int vk_gemm_ws(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, siz
 size_t vk_gemm_workspace_bytes(int version, vk_dtype in_dtype, size_t m, size_t n, size_t k) {
   const vk::KernelEntry* e = vk::find(version, in_dtype);
   if (!e || !e->workspace) return 0;
-  return e->workspace(m, n, k);
+  // The stream-K schedule depends on the current device's compute-unit count;
+  // with no device to ask, an MI355X (256 CUs) is assumed.
+  int cus = 256, dev = 0;
+  vk::DeviceState* ds = nullptr;
+  if (hipGetDevice(&dev) == hipSuccess && vk::device_state(dev, &ds) == hipSuccess) cus = ds->num_cus;
+  return e->workspace(m, n, k, cus);
 }
 
 const char* vk_gemm_name(int version, vk_dtype in_dtype) {

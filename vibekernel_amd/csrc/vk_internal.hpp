@@ -31,7 +31,8 @@ struct GemmArgs {
 };
 
 using LaunchFn = hipError_t (*)(const GemmArgs&);
-using WorkspaceFn = size_t (*)(size_t m, size_t n, size_t k);
+// Workspace bytes for one call; num_cus is the device's compute-unit count.
+using WorkspaceFn = size_t (*)(size_t m, size_t n, size_t k, int num_cus);
 // Optional extra shape rule beyond the divisibility in caps (nullptr = none).
 using ShapeFn = bool (*)(size_t m, size_t n, size_t k);
 

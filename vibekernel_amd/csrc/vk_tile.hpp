@@ -34,18 +34,27 @@ __host__ __device__ constexpr int swz_b(int krow) {
 // XCD bid % 8; the remap gives each XCD a contiguous range of the raster, and
 // the raster walks GM tile-rows at a time so neighbouring tiles share panels
 // of A and B in that XCD's L2.
-__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
-  const int total = tiles_m * tiles_n;
-  int cid = bid;
-  if ((total & 7) == 0) cid = (bid & 7) * (total >> 3) + (bid >> 3);
+// raster_tile: position `cid` of the grouped raster -> tile (tm, tn).
+__host__ __device__ __forceinline__ void raster_tile(int cid, int tiles_m, int tiles_n, int& tm, int& tn) {
   constexpr int GM = 4;
   const int group = GM * tiles_n;
   const int g = cid / group;
   const int first_m = g * GM;
-  const int gm = min(tiles_m - first_m, GM);
+  const int gm = tiles_m - first_m < GM ? tiles_m - first_m : GM;
   const int r = cid - g * group;
   tm = first_m + r % gm;
   tn = r / gm;
+}
+
+// Raster position of workgroup `bid`: with a tile count divisible by 8, XCD x
+// (= bid % 8) gets positions [x * total / 8, (x + 1) * total / 8) in launch
+// order; otherwise the identity.
+__host__ __device__ __forceinline__ int xcd_remap(int bid, int total) {
+  return (total & 7) == 0 ? (bid & 7) * (total >> 3) + (bid >> 3) : bid;
+}
+
+__device__ __forceinline__ void tile_of(int bid, int tiles_m, int tiles_n, int& tm, int& tn) {
+  raster_tile(xcd_remap(bid, tiles_m * tiles_n), tiles_m, tiles_n, tm, tn);
 }
 
 // hipFuncSetAttribute(MaxDynamicSharedMemorySize) once per kernel instance

@@ -97,13 +97,18 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
     """The fastest version that accepts this shape (checked with vk_gemm_check
     on 4 KiB-aligned placeholder addresses; nothing is launched): for fp16
     the skinny kernel when M <= 64, then the 256x256 kernels (fastest first), then
-    the any-shape kernel.  The reference picks versions at build time only
-    (CMakeLists.txt MATMUL_VERSION); this is a convenience of the front end."""
+    the any-shape kernel.  The stream-K version 9 comes first among the 256x256
+    kernels only where its schedule splits tiles on this device (it then needs
+    a workspace); elsewhere it would run version 7's whole tiles.  The
+    reference picks versions at build time only (CMakeLists.txt
+    MATMUL_VERSION); this is a convenience of the front end."""
     in_dt = DTYPE_F16 if dtype == "f16" else DTYPE_F32
     out_dt = DTYPE_F16 if (out or dtype) == "f16" else DTYPE_F32
-    order = [8, 4, 7, 6, 5, 3, 2, 1] if in_dt == DTYPE_F16 else [1]
+    order = [8, 4, 9, 7, 6, 5, 3, 2, 1] if in_dt == DTYPE_F16 else [1]
     avail = set(_abi.versions(in_dt))
     for v in order:
+        if v == 9 and _abi.workspace_bytes(v, in_dt, m, n, k) == 0:
+            continue
         if v in avail and _abi.check(v, in_dt, out_dt, m, n, k, 4096, 4096, 4096) == _abi.VK_OK:
             return v
     raise VkError(-3, f"no {dtype} version accepts m={m}, n={n}, k={k}")
