@@ -89,6 +89,11 @@ int vk_gemm_ws(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, siz
                const void* A, const void* B, void* C, void* workspace, size_t workspace_bytes,
                void* stream);
 
+/* Workspace bytes a call of this version and shape needs on the current
+ * device (0: none).  Version 9's depends on the device's compute-unit count;
+ * with no device to ask, an MI355X's 256 CUs are assumed.  No counterpart in
+ * the reference, whose versions keep such buffers in function-local statics
+ * (matmul_f16_v42_shfl2.cu:496-519). */
 size_t vk_gemm_workspace_bytes(int version, vk_dtype in_dtype, size_t m, size_t n, size_t k);
 
 /* Short name of a version ("f16_v2_dma256", ...), or NULL if unknown. */
