@@ -330,7 +330,7 @@ def main():
         "config": {
             "workload": f"{workload} row-major NN, fp32 accumulate, {out} out, "
                     f"{DIST_TEXT[args.dist]} seed {args.seed}",
-            "preset": args.workload,
+            "preset": args.workload if (m, n, k, dtype) == WORKLOADS[args.workload][:4] else "custom",
             "m": m, "n": n, "k": k,
             "version": version,
             "kernel": kname,

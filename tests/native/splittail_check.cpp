@@ -1,11 +1,11 @@
-// Host-side check of version 9's tail schedule (vk_streamk.hpp): simulates
+// Host-side check of version 9's tail schedule (vk_splittail.hpp): simulates
 // every workgroup of a launch for many tile counts, k-depths and CU counts --
 // for the plan sk_plan chooses and for every other admissible piece count --
 // and checks that the pieces cover each (tile, k-iteration) exactly once and
 // that the pieces of a split tile agree on where they meet.
 // Prints "ok <cases> <split plans>" or the first violation; exit status 1 on a
 // violation.
-#include "vk_streamk.hpp"
+#include "vk_splittail.hpp"
 
 #include <cstdio>
 #include <set>

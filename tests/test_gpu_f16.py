@@ -220,7 +220,7 @@ def test_square8192_normal05(gpu, oracle):
 @pytest.mark.parametrize("shape", [(4096, 11008, 4096), (4096, 4096, 11008)])
 def test_mlp_shapes(gpu, oracle, shape, version):
     """The MLP projections (up: 688 tiles of 256 x 256 = 2.69 waves on 256
-    CUs, which version 9 runs as 512 whole tiles plus a stream-K tail; down:
+    CUs, whose tail version 9 leaves whole, as version 7; down:
     one wave of 256 deep tiles): fp32 output against the oracle within the
     fp32 accumulation bound, fp16 output equal to its rounding."""
     m, n, k = shape

@@ -1,8 +1,8 @@
 """Version 9 (version 7's tile loop with a split tail) on the GPU, through the
 C ABI.  The schedule's own arithmetic is checked on the host
-(test_streamk_sched.py); here the split tiles' hand-off runs for real.
+(test_splittail_sched.py); here the split tiles' hand-off runs for real.
 
-Shapes and their plans on 256 CUs (vk_streamk.hpp):
+Shapes and their plans on 256 CUs (vk_splittail.hpp):
   2048 x 2048 x 4096    64 tiles x 4 pieces = 256 units, dealt per XCD
   768 x 2560 x 4096     30 tiles x 4 pieces = 120 units, one chunk
   1024 x 1280 x 2752    20 tiles of 43 k-tiles x 4 pieces of 10/10/10/13
@@ -32,7 +32,7 @@ def _ws(m, n, k):
 
 
 @pytest.mark.parametrize("shape", SK_SHAPES)
-def test_streamk_schedule_active(gpu, shape):
+def test_splittail_schedule_active(gpu, shape):
     """Each shape really runs split tiles on this device (a workspace is
     needed only then)."""
     assert _ws(*shape) > 0
@@ -40,7 +40,7 @@ def test_streamk_schedule_active(gpu, shape):
 
 @pytest.mark.parametrize("shape", SK_SHAPES)
 @pytest.mark.parametrize("out", ["f16", "f32"])
-def test_streamk_integer_kat_bit_exact(gpu, shape, out):
+def test_splittail_integer_kat_bit_exact(gpu, shape, out):
     m, n, k = shape
     A, B = make_inputs(m, n, k, "int", seed=m + 3 * n + 5 * k)
     # Entries in [-2, 2] and k <= 8192: every partial sum is an integer below
@@ -55,7 +55,7 @@ def test_streamk_integer_kat_bit_exact(gpu, shape, out):
 
 @pytest.mark.parametrize("shape", SK_SHAPES)
 @pytest.mark.parametrize("dist", ["uniform", "normal"])
-def test_streamk_random_vs_oracle(gpu, oracle, shape, dist):
+def test_splittail_random_vs_oracle(gpu, oracle, shape, dist):
     m, n, k = shape
     A, B = make_inputs(m, n, k, dist, seed=9 * m + n + k)
     C64 = oracle.dgemm(A, B)
@@ -67,7 +67,7 @@ def test_streamk_random_vs_oracle(gpu, oracle, shape, dist):
 
 
 @pytest.mark.parametrize("out", ["f16", "f32"])
-def test_streamk_whole_wave_equals_v7(gpu, out):
+def test_splittail_whole_wave_equals_v7(gpu, out):
     """4096^3 is one full wave on 256 CUs: no split tiles, and the same tile
     loop as version 7, so the results are bit-identical."""
     m = n = k = 4096
@@ -76,7 +76,7 @@ def test_streamk_whole_wave_equals_v7(gpu, out):
     assert np.array_equal(run_gemm(9, A, B, out).view(np.uint8), run_gemm(7, A, B, out).view(np.uint8))
 
 
-def test_streamk_repeat_and_reshape(gpu):
+def test_splittail_repeat_and_reshape(gpu):
     """90 launches cycling over three schedules (different unit counts, chunk
     dealing and counters) with C poisoned before each: every result bitwise
     equal to that shape's first.  Counters left non-zero by any call, or a
@@ -100,7 +100,7 @@ def test_streamk_repeat_and_reshape(gpu):
     torch.cuda.synchronize()
 
 
-def test_streamk_caller_workspace(gpu):
+def test_splittail_caller_workspace(gpu):
     """vk_gemm_ws with a caller workspace full of garbage: the launch clears
     the counters it keeps there, so the result equals the library-workspace
     call; a workspace one word short is refused."""

@@ -1,5 +1,5 @@
-"""The stream-K schedule of version 9 (vibekernel_amd/csrc/vk_streamk.hpp) on
-the host: tests/native/sk_sched_check.cpp simulates every workgroup of a
+"""The split-tail schedule of version 9 (vibekernel_amd/csrc/vk_splittail.hpp) on
+the host: tests/native/splittail_check.cpp simulates every workgroup of a
 launch for ~55k (tile count, k-depth, CU count) cases and checks exact
 coverage of every (tile, k-iteration), the meeting points of a split tile's
 pieces (piece order, partial slots, counters) and the per-XCD dealing.  The
@@ -19,16 +19,16 @@ HIPCC = shutil.which("hipcc") or "/opt/rocm/bin/hipcc"
 def sk_check(tmp_path_factory):
     if not os.path.exists(HIPCC):
         pytest.skip("hipcc not found")
-    out = str(tmp_path_factory.mktemp("sk") / "sk_sched_check")
-    src = os.path.join(ROOT, "tests", "native", "sk_sched_check.cpp")
+    out = str(tmp_path_factory.mktemp("sk") / "splittail_check")
+    src = os.path.join(ROOT, "tests", "native", "splittail_check.cpp")
     subprocess.run([HIPCC, "-O2", "-std=c++17", "-I" + CSRC, src, "-o", out], check=True,
                    capture_output=True, timeout=300)
     return out
 
 
-def test_streamk_schedule_invariants(sk_check):
+def test_splittail_schedule_invariants(sk_check):
     r = subprocess.run([sk_check], capture_output=True, text=True, timeout=300)
     assert r.returncode == 0, r.stdout + r.stderr
     assert r.stdout.startswith("ok "), r.stdout
-    # the check exercised stream-K plans, not only whole-tile ones
+    # the check exercised split plans, not only whole-tile ones
     assert int(r.stdout.split()[3]) > 1000, r.stdout

@@ -35,7 +35,7 @@
 // Both groups pass the same number of barriers: 1 + 1 + 2 nk + 1.
 #include "vk_device.hpp"
 #include "vk_internal.hpp"
-#include "vk_streamk.hpp"
+#include "vk_splittail.hpp"
 #include "vk_tile.hpp"
 
 #include <algorithm>
@@ -814,7 +814,7 @@ hipError_t launch(const GemmArgs& a) {
 // wave of 256x256 tiles would leave compute units idle (the reference's
 // answer to the same problem is stream-K, results/naive_fable_cycle2/src/
 // matmul_f16/matmul_f16_v9_streamk.cu:383-448, and the tail lesson of
-// matmul_f16_v42_shfl2.cu:182-189).  The schedule (vk_streamk.hpp): whole
+// matmul_f16_v42_shfl2.cu:182-189).  The schedule (vk_splittail.hpp): whole
 // tiles first, in version 7's order, then each tail tile cut into s aligned
 // k-slices computed by s workgroups at once.  The pieces of a split tile are
 // summed by whichever of them finishes last:
@@ -1009,7 +1009,7 @@ void register_f16_pingpong() {
 
   KernelEntry e9 = e7;
   e9.version = 9;
-  e9.name = "f16_v9_pp256_streamk";
+  e9.name = "f16_v9_pp256_splittail";
   e9.caps.version = 9;
   e9.caps.uses_workspace = 1;
   e9.launch = pp16::launch_sk;

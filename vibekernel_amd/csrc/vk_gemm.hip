@@ -205,7 +205,7 @@ int vk_gemm_ws(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, siz
 size_t vk_gemm_workspace_bytes(int version, vk_dtype in_dtype, size_t m, size_t n, size_t k) {
   const vk::KernelEntry* e = vk::find(version, in_dtype);
   if (!e || !e->workspace) return 0;
-  // The stream-K schedule depends on the current device's compute-unit count;
+  // The split-tail schedule depends on the current device's compute-unit count;
   // with no device to ask, an MI355X (256 CUs) is assumed.
   int cus = 256, dev = 0;
   vk::DeviceState* ds = nullptr;

@@ -1,4 +1,4 @@
-// vk_streamk.hpp -- the tail schedule of the 256x256-tile fp16 GEMM
+// vk_splittail.hpp -- the tail schedule of the 256x256-tile fp16 GEMM
 // (version 9): which workgroup computes which k-range of which tile, and
 // where the pieces of a split tile meet.  Host and device code share these
 // functions, so the launch, the kernel and the schedule's own tests agree.

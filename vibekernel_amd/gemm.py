@@ -97,7 +97,7 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
     """The fastest version that accepts this shape (checked with vk_gemm_check
     on 4 KiB-aligned placeholder addresses; nothing is launched): for fp16
     the skinny kernel when M <= 64, then the 256x256 kernels (fastest first), then
-    the any-shape kernel.  The stream-K version 9 comes first among the 256x256
+    the any-shape kernel.  The split-tail version 9 comes first among the 256x256
     kernels only where its schedule splits tiles on this device (it then needs
     a workspace); elsewhere it would run version 7's whole tiles.  The
     reference picks versions at build time only (CMakeLists.txt
