@@ -24,9 +24,14 @@
 //    workspace, device-scope atomic after the partials are complete) sums the
 //    KS partials in k order -- the same order whichever workgroup arrives
 //    last, so results are bit-reproducible -- writes C and resets the counter.
-//  * workgroup -> (column block, k part): the KS parts of a column block run
-//    on one XCD (workgroup b runs on XCD b % 8), so their partials meet in
-//    one L2.
+//  * workgroup b computes k part b % KS of column block b / KS, so the KS
+//    parts of a column block run on KS different XCDs (workgroup b runs on
+//    XCD b % 8).  Measured against dealing each XCD a contiguous run of
+//    column blocks (all KS parts of a block on one XCD): 24.8 vs 25.3 us per
+//    launch at 16 x 8192 x 8192.  Per-workgroup timelines show the XCDs
+//    themselves streaming at different rates (the slowest ~1.3x the fastest
+//    under either dealing), which is what keeps the kernel at ~0.8 of the
+//    streaming limit: the last workgroups end ~4 us after the mean.
 #include "vk_device.hpp"
 #include "vk_internal.hpp"
 #include "vk_tile.hpp"
@@ -97,10 +102,7 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
-  // Workgroup -> (column block, k part): consecutive ids per XCD.
-  const int grid = gridDim.x;
-  int cid = blockIdx.x;
-  if ((grid & 7) == 0) cid = (blockIdx.x & 7) * (grid >> 3) + (blockIdx.x >> 3);
+  const int cid = blockIdx.x;
   const int cb = cid / ks_count, kp = cid - cb * ks_count;
   const int n0 = cb * NC;
   const int kc = K / ks_count;  // k rows of this workgroup
