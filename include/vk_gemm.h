@@ -78,7 +78,10 @@ typedef struct vk_caps {
 /* C = A . B on `stream`.  Library-managed workspace: a version that needs one
  * allocates it on its first call on a device (like the reference's
  * function-local statics, matmul_f16_v42_shfl2.cu:496-519) and keeps it until
- * vk_gemm_release() or process exit. */
+ * vk_gemm_release() or process exit.  All calls of such versions on one
+ * device share that workspace, so they must not run concurrently (issue them
+ * on one stream, or order them); concurrent callers pass their own
+ * workspaces to vk_gemm_ws. */
 int vk_gemm(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, size_t n, size_t k,
             const void* A, const void* B, void* C, void* stream);
 
