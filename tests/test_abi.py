@@ -123,4 +123,5 @@ def test_pick_version_follows_shape():
     assert vk.pick_version(3840, 4096, 4096) == 7   # 240 of 256 CUs busy: not worth a split
     assert vk.pick_version(4096, 4096, 4128) == 5  # k % 64 != 0: the 32-deep kernel
     assert vk.pick_version(100, 300, 70) == 1
-    assert vk.pick_version(512, 512, 512, "f32") == 1
+    assert vk.pick_version(512, 512, 512, "f32") == 2   # fp32 on the matrix cores
+    assert vk.pick_version(500, 512, 512, "f32") == 1   # m % 256 != 0: the VALU kernel

@@ -38,6 +38,7 @@ void init_registry() {
     register_f16_pingpong();
     register_f16_skinny_sk();
     register_f32_valu();
+    register_f32_mfma();
   });
 }
 

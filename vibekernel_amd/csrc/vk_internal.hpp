@@ -59,6 +59,7 @@ void register_f16_skinny();
 void register_f16_pingpong();
 void register_f16_skinny_sk();
 void register_f32_valu();
+void register_f32_mfma();
 
 inline vk_caps make_caps(int version, vk_dtype in, int out_mask, uint32_t dm, uint32_t dn,
                          uint32_t dk, uint32_t align, uint32_t tm, uint32_t tn, uint32_t tk,
