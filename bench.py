@@ -28,7 +28,7 @@ Other configurations of the same GEMM: `--workload` (see WORKLOADS) or
 explicit --m/--n/--k/--dtype/--dist.
 
 Prints ONE JSON line.  Extra objects:
-  roofline     -- the kernel against its bound: dense fp16 MFMA peak (TFLOP/s),
+  roofline     -- the kernel against its bound: dense fp16 or fp32 peak (TFLOP/s),
                   or HBM bandwidth (GB/s) when the GEMM's arithmetic intensity
                   is below the ridge point; `traffic` (HBM bytes per launch) from
                   the committed rocprofv3 counter summary in profiles/, else null;
@@ -48,7 +48,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 PEAK_F16_TFLOPS = 2516.6   # 256 CU x 4096 FLOP/clk (dense fp16 MFMA) x 2.4 GHz
-PEAK_F32_TFLOPS = 157.3    # published fp32 figure (the VALU kernel reaches at most half: no packed FMA)
+PEAK_F32_TFLOPS = 157.3    # published dense fp32 figure (matrix cores and vector FMAs alike)
 PEAK_HBM_GBS = 8000.0
 METRIC = "sustained fp16 GEMM TFLOPS at 4096³ (100-iter avg) + % of MFMA peak"
 
@@ -304,7 +304,7 @@ def main():
         }
     else:
         roofline = {
-            "bound": "mfma" if dtype == "f16" else "valu",
+            "bound": "valu" if "valu" in kname else "mfma",
             "achieved": round(tflops, 2),
             "peak": peak,
             "unit": "TFLOP/s",
