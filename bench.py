@@ -202,7 +202,15 @@ def main():
     m, n, k = args.m, args.n, args.k
     dtype = args.dtype
     out = args.out or dtype
-    version = args.version if args.version is not None else vk.pick_version(m, n, k, dtype, out)
+    if args.version is not None:
+        version = args.version
+    elif dtype == "f32":
+        # The fp32 configuration is defined on the vector ALUs (a
+        # register-blocked VALU SGEMM, the CUDA-core-tier analog); the
+        # matrix-core fp32 kernel (version 2) is measured with --version 2.
+        version = 1
+    else:
+        version = vk.pick_version(m, n, k, dtype, out)
     kname = vk.name(version, dtype)
     if kname is None:
         print(f"bench.py: unknown {dtype} version {version}", file=sys.stderr)
