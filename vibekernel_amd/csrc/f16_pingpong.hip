@@ -863,7 +863,7 @@ __device__ __forceinline__ bool sk_arrive(float4v (&acc)[8][4], int np, int p, _
   const uint32_t soff = part_off(p);
 #pragma unroll
   for (int b = 0; b < 32; b++) store_partial(part, (uint32_t)lane * 16 + b * 1024, soff, acc[b >> 2][b & 3]);
-  wait_vmcnt<0>();  // the partial is in memory before the counter moves
+  wait_vmcnt0_ordered();  // the partial is in memory before the counter moves
   unsigned old = 0;
   if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   return __builtin_amdgcn_readfirstlane(old) == (unsigned)(np - 1);
@@ -877,6 +877,9 @@ __device__ __forceinline__ void sk_write_c(float4v (&acc)[8][4], int np, int p, 
                                            PartOff part_off, unsigned* cnt, uint32_t wstage, OutT* Cw, int N) {
   const int lane = lane_from_exec();
   const uint32_t vlane = (uint32_t)lane * 16;
+  // The counter read that made this wave the last stays before the reads of
+  // the other pieces' partials.
+  asm volatile("" ::: "memory");
   // C = P0 + P1 + ... + P(np-1), left to right, with P(p) = acc, summed 8
   // blocks at a time (the 8 loads of a piece issued together) and staged for
   // the store as each batch completes.

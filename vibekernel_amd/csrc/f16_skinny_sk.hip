@@ -211,7 +211,7 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
       for (int e = 0; e < 4; e++)
         __hip_atomic_store(&mine[(size_t)(16 * r + 4 * (lane >> 4) + e) * NC + G::kWaveCols * wave + 16 * c + (lane & 15)],
                            acc[r][c][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  wait_vmcnt<0>();
+  wait_vmcnt0_ordered();  // every wave's partial is in memory before the barrier and the counter
 
   // The last arrival of the column block reduces.
   __shared__ int s_last;

@@ -132,6 +132,12 @@ __device__ __forceinline__ void wait_vmcnt() {
 
 __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc07f); }
 
+// vmcnt(0) that is also a compiler barrier for memory accesses: stores
+// before it stay before it, and a counter update after it stays after it.
+// (The s_waitcnt builtin is modelled as touching no memory.)  For hand-offs
+// through global memory: the data stores must be complete before the flag.
+__device__ __forceinline__ void wait_vmcnt0_ordered() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // Workgroup barrier for LDS producer/consumer hand-off only: waits for this
 // wave's LDS reads (lgkmcnt) but, unlike __syncthreads(), not for its
 // in-flight global->LDS prefetches (vmcnt), which are waited for explicitly.
