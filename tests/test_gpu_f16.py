@@ -313,3 +313,44 @@ def test_skinny_rejects_wide_m(gpu, version):
     with pytest.raises(vk.VkError) as e:
         vk.matmul(80, 128, 128, A, B, C, version)
     assert e.value.status == -3
+
+
+@pytest.mark.slow
+@pytest.mark.parametrize("version", [7, 9])
+def test_headline_4096_integer_exact(gpu, version):
+    """Every element at the full headline size, bit for bit: integer inputs in
+    [-2, 2] keep every partial sum an integer below 2^15, exact in fp32
+    whatever the summation order, so the fp32-output C must equal the exact
+    product (computed in fp64 by BLAS, itself exact for these values)."""
+    m = n = k = 4096
+    A, B = make_inputs(m, n, k, "int", seed=4096)
+    exact = A.astype(np.float64) @ B.astype(np.float64)
+    C = run_gemm(version, A, B, "f32")
+    assert np.array_equal(C.astype(np.float64), exact)
+
+
+@pytest.mark.slow
+def test_headline_4096_transpose_and_split_invariants(gpu, oracle):
+    """(A.B)^T = B^T.A^T and C = A[:, :K/2].B[:K/2] + A[:, K/2:].B[K/2:] at
+    4096^3 on the default kernel, random fp16 inputs, fp32 output.  The
+    transposed problem forms the same products and sums them in the same k
+    order (k-tiles ascending, the MFMA's own reduction over its 32 k), so it
+    is bit-identical; the k-split adds two half sums, so it is held to the
+    fp32 accumulation bound (2 x 2 k u |A||B|)."""
+    import vibekernel_amd as vk
+    version = vk.DEFAULT_F16_VERSION
+    m = n = k = 4096
+    A, B = make_inputs(m, n, k, "uniform", seed=77)
+    C = run_gemm(version, A, B, "f32")
+    absAB = oracle.sgemm(np.abs(A.astype(np.float32)), np.abs(B.astype(np.float32))).astype(np.float64)
+    bound = 2 * 2 * k * 2.0 ** -24 * absAB
+    Ct = run_gemm(version, np.ascontiguousarray(B.T), np.ascontiguousarray(A.T), "f32")
+    diff_t = np.abs(Ct.T.astype(np.float64) - C)
+    print(f"transpose: max |diff| {diff_t.max():.3e}")
+    assert np.array_equal(Ct.T, C)
+    h = k // 2
+    C1 = run_gemm(version, np.ascontiguousarray(A[:, :h]), np.ascontiguousarray(B[:h]), "f32")
+    C2 = run_gemm(version, np.ascontiguousarray(A[:, h:]), np.ascontiguousarray(B[h:]), "f32")
+    diff_s = np.abs((C1.astype(np.float64) + C2) - C)
+    print(f"k-split: max |diff| {diff_s.max():.3e}")
+    assert np.all(diff_s <= bound)
