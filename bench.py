@@ -60,6 +60,7 @@ WORKLOADS = {
     "mlp_down": (4096, 4096, 11008, "f16", "uniform"),
     "square8192": (8192, 8192, 8192, "f16", "normal0.5"),
     "skinny": (16, 8192, 8192, "f16", "uniform"),
+    "skinny128": (128, 8192, 8192, "f16", "uniform"),
     "f32_4096": (4096, 4096, 4096, "f32", "uniform"),
     "f32_512": (512, 512, 512, "f32", "uniform"),
 }

@@ -116,6 +116,8 @@ def test_pick_version_follows_shape():
     import vibekernel_amd as vk
     assert vk.pick_version(16, 8192, 8192) == 8
     assert vk.pick_version(16, 8224, 8192) == 4  # n % 128 != 0: the 32-column kernel
+    assert vk.pick_version(128, 8192, 8192) == 8  # batch-128 decode: still the split-K kernel
+    assert vk.pick_version(144, 8192, 8192) == 1  # beyond 128 rows: the any-shape kernel
     assert vk.pick_version(4096, 4096, 4096) == 7  # 256 tiles: one full wave
     assert vk.pick_version(4096, 4096, 4096, "f16", "f32") == 7
     assert vk.pick_version(4096, 11008, 4096) == 7  # 688 tiles = 2.69 waves: tail left whole

@@ -18,7 +18,8 @@ pytestmark = pytest.mark.gpu
 
 TILE_SHAPES = [(256, 256, 64), (512, 256, 128), (256, 512, 192), (768, 512, 256), (1024, 1024, 512)]
 ANY_SHAPES = [(1, 1, 1), (17, 33, 65), (127, 129, 31), (200, 300, 100), (256, 256, 64), (64, 8, 1000)]
-SKINNY_SHAPES = [(16, 256, 512), (32, 512, 1024), (48, 96, 128), (64, 128, 256), (16, 2048, 4096)]
+SKINNY_SHAPES = [(16, 256, 512), (32, 512, 1024), (48, 96, 128), (64, 128, 256), (16, 2048, 4096),
+                 (80, 256, 512), (96, 384, 96), (112, 128, 1024), (128, 1024, 2048)]
 
 
 def _versions():
@@ -32,7 +33,7 @@ def _shapes_for(version):
     shapes = [s for s in TILE_SHAPES if s[0] % c.div_m == 0 and s[1] % c.div_n == 0 and s[2] % c.div_k == 0]
     if c.div_m == 1 and c.div_n == 1 and c.div_k == 1:
         shapes = ANY_SHAPES + shapes[:2]
-    if c.max_m <= 64:
+    if c.max_m <= 128:
         shapes = [s for s in SKINNY_SHAPES if s[0] <= c.max_m and s[0] % c.div_m == 0
                   and s[1] % c.div_n == 0 and s[2] % c.div_k == 0]
     return shapes
@@ -234,11 +235,11 @@ def test_mlp_shapes(gpu, oracle, shape, version):
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("version", [4, 8])
-def test_skinny_decode_shape(gpu, oracle, version):
-    """M = 16, N = K = 8192 (the decode-like, HBM-bound configuration) on the
-    skinny kernels, fp16 and fp32 output, against the oracle."""
-    m, n, k = 16, 8192, 8192
+@pytest.mark.parametrize("version,m", [(4, 16), (8, 16), (8, 128)])
+def test_skinny_decode_shape(gpu, oracle, version, m):
+    """M = 16 or 128, N = K = 8192 (the decode-like, HBM-bound configurations)
+    on the skinny kernels, fp16 and fp32 output, against the oracle."""
+    n, k = 8192, 8192
     A, B = make_inputs(m, n, k, "uniform", seed=16)
     C64 = oracle.dgemm(A, B)
     C32 = run_gemm(version, A, B, "f32")
@@ -259,7 +260,7 @@ def test_splitk_skinny_repeat_and_reshape(gpu):
     import torch
     import vibekernel_amd as vk
     g = torch.Generator(device="cuda:0").manual_seed(8)
-    shapes = [(16, 8192, 8192), (64, 1024, 2048), (32, 384, 96)]
+    shapes = [(16, 8192, 8192), (64, 1024, 2048), (32, 384, 96), (128, 2048, 4096), (80, 512, 1024)]
     data = []
     for m, n, k in shapes:
         A = (torch.rand((m, k), generator=g, device="cuda:0") * 2 - 1).half()
@@ -274,6 +275,19 @@ def test_splitk_skinny_repeat_and_reshape(gpu):
         vk.matmul(m, n, k, A, B, C, 8)
         assert torch.equal(C, ref), f"call {it}: m={m} n={n} k={k}"
     torch.cuda.synchronize()
+
+
+def test_splitk_skinny_shape_sequence(gpu, oracle):
+    """Version 8 through the library workspace over shapes whose numbers of
+    column blocks and k parts differ, narrow to wide and back: each call's
+    partials must leave the next call's counters zero (they once overlapped
+    the counters of a wider call), so every call matches the oracle."""
+    shapes = [(16, 128, 4096), (128, 256, 2048), (16, 8192, 8192), (32, 28672, 1024), (48, 384, 2048),
+              (128, 8192, 1024), (16, 128, 4096)]
+    for m, n, k in shapes:
+        A, B = make_inputs(m, n, k, "uniform", seed=m + n + k)
+        C = run_gemm(8, A, B, "f32")
+        check_f32_out(C, A, B, oracle.dgemm(A, B))
 
 
 def test_splitk_skinny_caller_workspace(gpu, oracle):
@@ -303,15 +317,15 @@ def test_splitk_skinny_caller_workspace(gpu, oracle):
     assert small == -6  # VK_ERR_WORKSPACE
 
 
-@pytest.mark.parametrize("version", [4, 8])
-def test_skinny_rejects_wide_m(gpu, version):
+@pytest.mark.parametrize("version,m", [(4, 80), (8, 144)])
+def test_skinny_rejects_wide_m(gpu, version, m):
     import torch
     import vibekernel_amd as vk
-    A = torch.zeros((80, 128), dtype=torch.float16, device="cuda:0")
+    A = torch.zeros((m, 128), dtype=torch.float16, device="cuda:0")
     B = torch.zeros((128, 128), dtype=torch.float16, device="cuda:0")
-    C = torch.zeros((80, 128), dtype=torch.float16, device="cuda:0")
+    C = torch.zeros((m, 128), dtype=torch.float16, device="cuda:0")
     with pytest.raises(vk.VkError) as e:
-        vk.matmul(80, 128, 128, A, B, C, version)
+        vk.matmul(m, 128, 128, A, B, C, version)
     assert e.value.status == -3
 
 

@@ -837,17 +837,8 @@ size_t sk_workspace(size_t m, size_t n, size_t k, int num_cus) {
   return p.units ? kSkCounterBytes + (size_t)p.units * kSkSlotBytes : 0;
 }
 
-// Partial slots are read and written through a buffer resource with the sc1
-// cache policy (the encoding of agent-scope atomic loads and stores): such
-// stores do not stay dirty in the writing XCD's L2, and such loads are not
-// served stale from the reading XCD's L2.
-constexpr int kCpolAgent = 16;  // sc1
-__device__ __forceinline__ void store_partial(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float4v v) {
-  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uint4v, v), r, voff, soff, kCpolAgent);
-}
-__device__ __forceinline__ float4v load_partial(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
-  return __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kCpolAgent));
-}
+// Partial slots are read and written with store_partial / load_partial (sc1
+// buffer accesses).
 
 // Hand-off of one wave's block of a tile split into np pieces; this wave holds
 // piece p.  part_off(q) is the byte offset of the wave's region of piece q's

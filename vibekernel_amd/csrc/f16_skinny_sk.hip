@@ -1,4 +1,4 @@
-// f16_skinny_sk.hip -- fp16 GEMM for skinny A (decode-like: M <= 64), version 8:
+// f16_skinny_sk.hip -- fp16 GEMM for skinny A (decode-like: M <= 128), version 8:
 // split-K over workgroups with a deterministic in-kernel reduction.
 //
 // Same job as version 4 (f16_skinny.hip); the reference has no path for this
@@ -14,16 +14,23 @@
 //    KS the power of two that brings the grid to 256 workgroups (KS = 4 at
 //    N = 8192);
 //  * 4 waves; per 32-deep k-step each wave loads 8 rows of B (direct-to-LDS,
-//    1 KB per instruction) and waves 0..MB-1 one 16-row block of A; a ring of
-//    up to 8 stages (7 k-steps of B in flight), one barrier per k-step;
+//    1 KB per instruction) and wave w the 16-row blocks w and w + 4 of A that
+//    exist (MB = M / 16 blocks); a ring of up to 8 stages (7 k-steps of B in
+//    flight), one barrier per k-step;
 //  * wave w computes columns w*NC/4 .. of the block (NC/64 blocks of 16) for
 //    all M rows with v_mfma_f32_16x16x32_f16 (A with ds_read_b128, B with the
 //    transpose read);
-//  * each workgroup writes its fp32 partial (M x NC) to the workspace; the
-//    last of the KS workgroups of a column block (a counter in the
-//    workspace, device-scope atomic after the partials are complete) sums the
-//    KS partials in k order -- the same order whichever workgroup arrives
+//  * each wave writes its fp32 partial (M x NC/4) to the workspace; the last
+//    of the KS waves holding the same columns (a counter per column block and
+//    wave in the workspace, device-scope atomic after the partial is complete)
+//    sums the KS partials in k order -- the same order whichever part arrives
 //    last, so results are bit-reproducible -- writes C and resets the counter.
+//    At M = 128 one workgroup's partial is 64 KB: the partials are laid out so
+//    that every access is a coalesced 1 KB row per wave instruction, and the
+//    last arrival keeps its own part in registers.  Measured at
+//    128 x 8192 x 8192 against one counter per column block and 4-byte
+//    accesses: the reductions at the end of the launch took 3.5-4.7 us
+//    instead of 9 us.
 //  * workgroup b computes k part b % KS of column block b / KS, so the KS
 //    parts of a column block run on KS different XCDs (workgroup b runs on
 //    XCD b % 8).  Measured against dealing each XCD a contiguous run of
@@ -59,7 +66,9 @@ struct SkCfg {
   static constexpr int kWaveCols = NC / kWaves;                 // 32 or 64
   static constexpr int kColBlocks = kWaveCols / 16;             // per wave
   static_assert(kStages >= 4, "pipeline depth");
-  static_assert((kStages - 1) * (kBDma + 1) <= 63, "vmcnt range");
+  static constexpr int kMaxADma = MB > kWaves ? 2 : 1;         // A loads per wave per k-step
+  static_assert(MB <= 2 * kWaves, "A blocks per k-step");
+  static_assert((kStages - 1) * (kBDma + kMaxADma) <= 63, "vmcnt range");
 };
 
 // Swizzles (physical chunk = logical chunk ^ f(row)), applied by choosing
@@ -111,8 +120,9 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
 
   // Direct-to-LDS duty per k-step.  B: load i covers k-rows 8w + i*R .. +R-1
   // (R = 1024 / (2 NC) rows of NC/8 chunks; lane l: row l / (NC/8), slot
-  // l % (NC/8)).  A: wave w < MB covers rows 16w .. 16w+15 (4 chunks each;
-  // lane l: row l/4, slot l%4).
+  // l % (NC/8)).  A: wave w covers rows 16w .. 16w+15 if w < MB and rows
+  // 16(w+4) .. +15 if w + 4 < MB (4 chunks each; lane l: row l/4, slot l%4;
+  // the swizzle of row r + 64 is that of row r).
   uint32_t offB[G::kBDma];
 #pragma unroll
   for (int i = 0; i < G::kBDma; i++) {
@@ -124,15 +134,18 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
   const uint32_t offA = (uint32_t)(((size_t)arow * K + (((lane & 3) ^ swz_a64(arow)) * 8)) * 2);
   const char* gB = reinterpret_cast<const char*>(B) + ((size_t)kbeg * N + n0) * 2;
   const char* gA = reinterpret_cast<const char*>(A) + (size_t)kbeg * 2;
+  const char* gA4 = gA + (size_t)64 * K * 2;  // rows 64 .. 127
   const uint32_t lbase = lds_addr32(lds);
-  const bool loads_a = wave < MB;
+  const int na = (wave < MB) + (wave + kWaves < MB);  // A loads of this wave per k-step (wave-uniform)
 
   auto issue = [&](int stage, int step) {
     const uint32_t s = lbase + stage * G::kStageBytes;
     const size_t kb = (size_t)step * kKStep;
 #pragma unroll
     for (int i = 0; i < G::kBDma; i++) dma16(gB + kb * N * 2, offB[i], s + (8 * wave + i * G::kRowsPerDma) * NC * 2);
-    if (loads_a) dma16(gA + kb * 2, offA, s + G::kBStageBytes + wave * 1024);
+    if (wave < MB) dma16(gA + kb * 2, offA, s + G::kBStageBytes + wave * 1024);
+    if (G::kMaxADma == 2 && wave + kWaves < MB)
+      dma16(gA4 + kb * 2, offA, s + G::kBStageBytes + (wave + kWaves) * 1024);
   };
 
   // Fragment addresses inside a stage.
@@ -167,7 +180,9 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
     const int stage = step % S;
     // This wave's loads of `step` landed, then everyone's (barrier); the
     // barrier also ends every wave's reads of the previous stage.
-    if (loads_a)
+    if (G::kMaxADma == 2 && na == 2)
+      wait_vmcnt<(S - 2) * (G::kBDma + G::kMaxADma)>();
+    else if (na >= 1)
       wait_vmcnt<(S - 2) * (G::kBDma + 1)>();
     else
       wait_vmcnt<(S - 2) * G::kBDma>();
@@ -181,93 +196,114 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
       const half4 hi = lds_read_tr16_at(sb + boff[c] + 4 * NC * 2);
       b[c] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
+    // All fragment reads go out before the first MFMA (the scheduler by
+    // itself reads A two blocks at a time, each pair waited for).
+    half8 a[MB];
 #pragma unroll
-    for (int r = 0; r < MB; r++) {
-      const half8 a = lds_read_h8(sb + aoff + r * 1024);
+    for (int r = 0; r < MB; r++) a[r] = lds_read_h8(sb + aoff + r * 1024);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int c = 0; c < G::kColBlocks; c++) acc[r][c] = mfma16x16x32(a, b[c], acc[r][c]);
-    }
+    for (int r = 0; r < MB; r++)
+#pragma unroll
+      for (int c = 0; c < G::kColBlocks; c++) acc[r][c] = mfma16x16x32(a[r], b[c], acc[r][c]);
   }
   wait_vmcnt<0>();  // clamped tail refills
 
-  // Partial of this workgroup: part[(cb * KS + kp)][16*MB rows][NC cols].
-  // D layout: lane l, register e -> row 4*(l/16) + e, column l%16 of the block.
-  //
-  // Cross-workgroup hand-off without a cache write-back: the partials are
-  // written and read with agent-scope coherent accesses (relaxed atomic
-  // stores and loads: global_store/global_load with sc1, which do not stay
-  // dirty in, or get served stale from, an XCD's own L2), and each wave
-  // waits until its stores have completed (vmcnt(0)) before the counter is
-  // incremented.  A __threadfence() would do the same by writing back the
-  // whole L2 of the XCD, which measured ~25 us per launch with 256
-  // workgroups fencing.
-  const size_t pstride = (size_t)16 * MB * NC;
-  float* mine = part + ((size_t)cb * ks_count + kp) * pstride;
+  // Epilogue.  D layout: lane l, register e of block (r, c) -> row
+  // 16 r + 4 (l / 16) + e, column kWaveCols * w + 16 c + l % 16 of the block.
+  constexpr int NB = MB * G::kColBlocks;  // 16 x 16 blocks per wave
+  OutT* Cw = C + n0 + G::kWaveCols * wave + (lane & 15);
+  const int rq = 4 * (lane >> 4);
+  auto store_c = [&](int b, const float4v& v) {
+    const int r = b / G::kColBlocks, c = b % G::kColBlocks;
 #pragma unroll
-  for (int r = 0; r < MB; r++)
+    for (int e = 0; e < 4; e++) Cw[(size_t)(16 * r + rq + e) * N + 16 * c] = convert_out<OutT>(v[e]);
+  };
+  if (ks_count == 1) {
 #pragma unroll
-    for (int c = 0; c < G::kColBlocks; c++)
-#pragma unroll
-      for (int e = 0; e < 4; e++)
-        __hip_atomic_store(&mine[(size_t)(16 * r + 4 * (lane >> 4) + e) * NC + G::kWaveCols * wave + 16 * c + (lane & 15)],
-                           acc[r][c][e], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  wait_vmcnt0_ordered();  // every wave's partial is in memory before the barrier and the counter
+    for (int b = 0; b < NB; b++) store_c(b, acc[b / G::kColBlocks][b % G::kColBlocks]);
+    return;
+  }
 
-  // The last arrival of the column block reduces.
-  __shared__ int s_last;
-  __syncthreads();
-  if (threadIdx.x == 0)
-    s_last = __hip_atomic_fetch_add(&counters[cb], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-             (unsigned)(ks_count - 1);
-  __syncthreads();
-  if (!s_last) return;
-  // Thread t owns column t % NC of rows t / NC, + RS, ..; loads are issued in
-  // batches of up to 64 before their (k-ordered) sums.
-  constexpr int RS = kThreads / NC;   // row step
-  constexpr int RPT = 16 * MB / RS;   // rows per thread
-  const float* col0 = part + (size_t)cb * ks_count * pstride;
-  const int col = threadIdx.x % NC;
-  const int r0 = threadIdx.x / NC;
-  auto reduce = [&](auto nparts) {
+  // Split K.  The partial of (column block cb, k part q) is slot cb * KS + q;
+  // wave w's region of a slot holds its NB blocks x 64 lanes x 16 bytes, so
+  // every partial access is a coalesced 1 KB row.  Each wave hands off on its
+  // own counter (cb, w): it first reads the counter, and if every other part
+  // has arrived it is the last and skips its store; otherwise it stores its
+  // partial, waits for the stores to complete, and increments the counter.
+  // The last arrival sums the KS parts in k order, its own from registers --
+  // the same sum whichever part arrives last -- writes C and resets the
+  // counter for the next call.
+  constexpr uint32_t kWaveRegion = NB * 1024;
+  constexpr uint32_t kSlotBytes = kWaves * kWaveRegion;
+  const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
+      part, 0, (int)((uint32_t)(N / NC) * (uint32_t)ks_count * kSlotBytes), kBufferWord3);
+  auto soff = [&](int q) { return (uint32_t)(cb * ks_count + q) * kSlotBytes + (uint32_t)wave * kWaveRegion; };
+  const uint32_t vlane = (uint32_t)lane * 16;
+  unsigned* cnt = counters + cb * kWaves + wave;
+  const unsigned seen =
+      __builtin_amdgcn_readfirstlane(__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  if (seen != (unsigned)(ks_count - 1)) {
+#pragma unroll
+    for (int b = 0; b < NB; b++) store_partial(prs, vlane + b * 1024, soff(kp), acc[b / G::kColBlocks][b % G::kColBlocks]);
+    wait_vmcnt0_ordered();  // the partial is in memory before the counter moves
+    unsigned old = 0;
+    if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (__builtin_amdgcn_readfirstlane(old) != (unsigned)(ks_count - 1)) return;
+  }
+  // The counter read that made this wave the last stays before the reads of
+  // the other parts.
+  asm volatile("" ::: "memory");
+  auto fold = [&](auto nparts) {
     constexpr int P = decltype(nparts)::value;
-    // rows per batch: the largest power of two that divides RPT, at most 64 / P
-    constexpr int RP2 = RPT & -RPT;
-    constexpr int RB = (64 / P < RP2) ? 64 / P : RP2;
-    static_assert(RPT % RB == 0, "row batches");
+    constexpr int BB = (32 / P < NB) ? 32 / P : NB;  // blocks per batch: up to 32 loads in flight
 #pragma unroll
-    for (int b0 = 0; b0 < RPT; b0 += RB) {
-      float x[P][RB];
+    for (int b0 = 0; b0 < NB; b0 += BB) {
+      float4v x[P][BB];
 #pragma unroll
-      for (int p = 0; p < P; p++)
+      for (int q = 0; q < P; q++) {
+        if (q != kp) {
 #pragma unroll
-        for (int i = 0; i < RB; i++)
-          x[p][i] = __hip_atomic_load(&col0[(size_t)p * pstride + (size_t)(r0 + RS * (b0 + i)) * NC + col],
-                                      __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          for (int i = 0; i < BB; i++)
+            if (b0 + i < NB) x[q][i] = load_partial(prs, vlane + (b0 + i) * 1024, soff(q));
+        } else {
 #pragma unroll
-      for (int i = 0; i < RB; i++) {
-        float v = 0.0f;
+          for (int i = 0; i < BB; i++)
+            if (b0 + i < NB) x[q][i] = acc[(b0 + i) / G::kColBlocks][(b0 + i) % G::kColBlocks];
+        }
+      }
 #pragma unroll
-        for (int p = 0; p < P; p++) v += x[p][i];
-        const int row = r0 + RS * (b0 + i);
-        if (row < M) C[(size_t)row * N + n0 + col] = convert_out<OutT>(v);
+      for (int i = 0; i < BB; i++) {
+        if (b0 + i < NB) {
+          float4v t = x[0][i];
+#pragma unroll
+          for (int q = 1; q < P; q++) t += x[q][i];
+          store_c(b0 + i, t);
+        }
       }
     }
   };
   switch (ks_count) {
-    case 1: reduce(std::integral_constant<int, 1>{}); break;
-    case 2: reduce(std::integral_constant<int, 2>{}); break;
-    case 4: reduce(std::integral_constant<int, 4>{}); break;
-    default: reduce(std::integral_constant<int, 8>{}); break;
+    case 2: fold(std::integral_constant<int, 2>{}); break;
+    case 4: fold(std::integral_constant<int, 4>{}); break;
+    default: fold(std::integral_constant<int, 8>{}); break;
   }
-  // Every part has arrived: reset for the next call.
-  if (threadIdx.x == 0) __hip_atomic_store(&counters[cb], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-size_t sk_counter_bytes(size_t n) { return ((n / 128) * sizeof(unsigned) + 255) & ~(size_t)255; }
+// Workspace: a fixed 4 KB of (column block, wave) counters, then the
+// partials.  K is split only while fewer than 256 column blocks exist
+// (pick_ks), so at most 255 x 4 counters are in use; the counters sit at the
+// same place for every shape, which keeps the library workspace clean (all
+// counters zero) from one call to the next whatever the shapes.  Unsplit
+// shapes need no workspace.
+constexpr size_t kCounterBytes = 4096;
 
 size_t sk_workspace(size_t m, size_t n, size_t k, int) {
-  const int mb = (int)((m + 15) / 16);
-  return sk_counter_bytes(n) + (size_t)pick_ks(n, k) * n * 16 * mb * sizeof(float);
+  const int ks = pick_ks(n, k);
+  if (ks == 1) return 0;
+  const size_t mb = (m + 15) / 16;
+  return kCounterBytes + (size_t)ks * n * 16 * mb * sizeof(float);
 }
 
 template <int NC, int MB, typename OutT>
@@ -278,11 +314,16 @@ hipError_t launch_sk_t(const GemmArgs& a) {
   hipError_t e = ensure_lds_attr(kfn, G::kLdsBytes, a.device, done);
   if (e != hipSuccess) return e;
   const int ks = pick_ks(a.n, a.k);
-  unsigned* counters = static_cast<unsigned*>(a.workspace);
-  float* part = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + sk_counter_bytes(a.n));
-  if (!a.workspace_clean) {
-    e = zero_words(counters, sk_counter_bytes(a.n) / 4, a.stream);
-    if (e != hipSuccess) return e;
+  unsigned* counters = nullptr;
+  float* part = nullptr;
+  if (ks > 1) {
+    if ((a.n / NC) * kWaves * sizeof(unsigned) > kCounterBytes) return hipErrorInvalidValue;
+    counters = static_cast<unsigned*>(a.workspace);
+    part = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + kCounterBytes);
+    if (!a.workspace_clean) {
+      e = zero_words(counters, kCounterBytes / 4, a.stream);
+      if (e != hipSuccess) return e;
+    }
   }
   const unsigned grid = (unsigned)((a.n / NC) * ks);
   hipLaunchKernelGGL(kfn, dim3(grid), dim3(kThreads), G::kLdsBytes, a.stream, static_cast<const half_t*>(a.A),
@@ -302,17 +343,21 @@ hipError_t launch_nc(const GemmArgs& a) {
     case 1: return launch_mb<NC, 1>(a);
     case 2: return launch_mb<NC, 2>(a);
     case 3: return launch_mb<NC, 3>(a);
-    default: return launch_mb<NC, 4>(a);
+    case 4: return launch_mb<NC, 4>(a);
+    case 5: return launch_mb<NC, 5>(a);
+    case 6: return launch_mb<NC, 6>(a);
+    case 7: return launch_mb<NC, 7>(a);
+    default: return launch_mb<NC, 8>(a);
   }
 }
 
 hipError_t launch_sk(const GemmArgs& a) { return launch_nc<128>(a); }
 
-// M a multiple of 16 up to 64; N a multiple of 128; K a multiple of 32; the
-// per-lane 32-bit byte offsets (up to 64 rows of A, 32 rows of B) must not
-// overflow.
+// M a multiple of 16 up to 128; N a multiple of 128; K a multiple of 32; the
+// per-lane 32-bit byte offsets (up to 64 rows of A from either base, 32 rows
+// of B) must not overflow.
 bool sk_shape_ok(size_t m, size_t n, size_t k) {
-  return m >= 16 && m <= 64 && (size_t)64 * k * 2 < (1ull << 31) && (size_t)32 * n * 2 < (1ull << 31) &&
+  return m >= 16 && m <= 128 && (size_t)64 * k * 2 < (1ull << 31) && (size_t)32 * n * 2 < (1ull << 31) &&
          (n / 128) * 8 < (1ull << 31);
 }
 
@@ -323,8 +368,8 @@ void register_f16_skinny_sk() {
   e.version = 8;
   e.in_dtype = VK_DTYPE_F16;
   e.name = "f16_v8_skinny_splitk";
-  e.caps = make_caps(8, VK_DTYPE_F16, kOutF16 | kOutF32, 16, 128, kKStep, 16, 64, 128, kKStep, kThreads,
-                     SkCfg<128, 4>::kLdsBytes, 0, 1, 64);
+  e.caps = make_caps(8, VK_DTYPE_F16, kOutF16 | kOutF32, 16, 128, kKStep, 16, 128, 128, kKStep, kThreads,
+                     SkCfg<128, 8>::kLdsBytes, 0, 1, 128);
   e.launch = launch_sk;
   e.workspace = sk_workspace;
   e.shape_ok = sk_shape_ok;

@@ -138,6 +138,19 @@ __device__ __forceinline__ void wait_lgkmcnt0() { __builtin_amdgcn_s_waitcnt(0xc
 // through global memory: the data stores must be complete before the flag.
 __device__ __forceinline__ void wait_vmcnt0_ordered() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 
+// Cross-workgroup partial sums are read and written through a raw buffer
+// resource with the sc1 cache policy (the encoding of agent-scope atomic loads
+// and stores): such stores do not stay dirty in the writing XCD's L2, and such
+// loads are not served stale from the reading XCD's L2.  16 bytes per lane, so
+// one wave instruction moves a coalesced 1 KB row.
+constexpr int kCpolAgent = 16;  // sc1
+__device__ __forceinline__ void store_partial(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff, float4v v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uint4v, v), r, voff, soff, kCpolAgent);
+}
+__device__ __forceinline__ float4v load_partial(__amdgpu_buffer_rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float4v, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, kCpolAgent));
+}
+
 // Workgroup barrier for LDS producer/consumer hand-off only: waits for this
 // wave's LDS reads (lgkmcnt) but, unlike __syncthreads(), not for its
 // in-flight global->LDS prefetches (vmcnt), which are waited for explicitly.
