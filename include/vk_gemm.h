@@ -93,7 +93,7 @@ int vk_gemm_ws(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, siz
                void* stream);
 
 /* Workspace bytes a call of this version and shape needs on the current
- * device (0: none).  Version 9's depends on the device's compute-unit count;
+ * device (0: none).  Versions 8 and 9 depend on the device's compute-unit count;
  * with no device to ask, an MI355X's 256 CUs are assumed.  No counterpart in
  * the reference, whose versions keep such buffers in function-local statics
  * (matmul_f16_v42_shfl2.cu:496-519). */

@@ -282,8 +282,8 @@ def test_splitk_skinny_shape_sequence(gpu, oracle):
     column blocks and k parts differ, narrow to wide and back: each call's
     partials must leave the next call's counters zero (they once overlapped
     the counters of a wider call), so every call matches the oracle."""
-    shapes = [(16, 128, 4096), (128, 256, 2048), (16, 8192, 8192), (32, 28672, 1024), (48, 384, 2048),
-              (128, 8192, 1024), (16, 128, 4096)]
+    shapes = [(16, 128, 4096), (128, 256, 2048), (16, 8192, 8192), (32, 28672, 1024), (16, 16384, 1024),
+              (48, 384, 2048), (128, 8192, 1024), (16, 128, 4096)]
     for m, n, k in shapes:
         A, B = make_inputs(m, n, k, "uniform", seed=m + n + k)
         C = run_gemm(8, A, B, "f32")

@@ -11,12 +11,13 @@
 // Version 4 owns 64-byte strips.  Here:
 //  * a workgroup owns NC = 128 columns (256-byte rows of B; the kernel is
 //    written for NC = 256 as well) and 1/KS of K; grid = (N / NC) x KS with
-//    KS the power of two that brings the grid to 256 workgroups (KS = 4 at
-//    N = 8192);
+//    KS the largest power of two (up to 8) that keeps the grid within one
+//    workgroup per CU (KS = 4 at N = 8192 on 256 CUs);
 //  * 4 waves; per 32-deep k-step each wave loads 8 rows of B (direct-to-LDS,
 //    1 KB per instruction) and wave w the 16-row blocks w and w + 4 of A that
-//    exist (MB = M / 16 blocks); a ring of up to 8 stages (7 k-steps of B in
-//    flight), one barrier per k-step;
+//    exist (MB = M / 16 blocks); a ring of up to 8 stages (6-7 k-steps of B
+//    in flight), one barrier per k-step, the fragment reads of one k-step
+//    overlapping the MFMAs of the one before;
 //  * wave w computes columns w*NC/4 .. of the block (NC/64 blocks of 16) for
 //    all M rows with v_mfma_f32_16x16x32_f16 (A with ds_read_b128, B with the
 //    transpose read);
@@ -90,12 +91,22 @@ __host__ __device__ constexpr int swz_a64(int row) { return (row >> 2) & 3; }
 // k-split costs more in the final reduction than the wider rows gain).
 int pick_nc(size_t) { return 128; }
 
-// Number of workgroups sharing a column block's K range: a power of two up
-// to 8 that brings the grid to 256 and divides K into 32-deep steps.
-int pick_ks(size_t n, size_t k) {
+// Counters of the split-K hand-off, one per (column block, wave).
+constexpr size_t kCounterBytes = 4096;
+
+// Number of workgroups sharing a column block's K range: the largest power
+// of two up to 8 that keeps the grid to one workgroup per CU and divides K
+// into 32-deep steps.  Measured (us per launch, K split 1/2/4/8 ways):
+// 128 x 28672 x 8192 (224 column blocks): 118 / 133 / 154 / 192;
+// 128 x 11008 x 4096 (86): 46 / 29 / 37 / 52; 32 x 14336 x 4096 (112):
+// 23 / 21 / 25 / 36; 128 x 8192 x 8192 (64): 86 / 49 / 33 / 54 -- a second
+// round of workgroups costs more than the longer k range of each.
+int pick_ks(size_t n, size_t k, int num_cus) {
   const size_t ncb = n / pick_nc(n);
   int ks = 1;
-  while (ks < 8 && ncb * ks < 256 && k % ((size_t)kKStep * ks * 2) == 0) ks *= 2;
+  while (ks < 8 && ncb * ks * 2 <= (size_t)num_cus && k % ((size_t)kKStep * ks * 2) == 0 &&
+         ncb * kWaves * sizeof(unsigned) <= kCounterBytes)
+    ks *= 2;
   return ks;
 }
 
@@ -171,41 +182,65 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
 #pragma unroll
     for (int c = 0; c < G::kColBlocks; c++) acc[r][c] = float4v{0.f, 0.f, 0.f, 0.f};
 
-  // Prologue: S-1 steps in flight (clamped refills of a short k range land in
-  // stages that are never read).
-#pragma unroll
-  for (int st = 0; st < S - 1; st++) issue(st, min(st, nsteps - 1));
-
-  for (int step = 0; step < nsteps; step++) {
-    const int stage = step % S;
-    // This wave's loads of `step` landed, then everyone's (barrier); the
-    // barrier also ends every wave's reads of the previous stage.
-    if (G::kMaxADma == 2 && na == 2)
-      wait_vmcnt<(S - 2) * (G::kBDma + G::kMaxADma)>();
-    else if (na >= 1)
-      wait_vmcnt<(S - 2) * (G::kBDma + 1)>();
-    else
-      wait_vmcnt<(S - 2) * G::kBDma>();
-    lds_barrier();
-    issue((step + S - 1) % S, min(step + S - 1, nsteps - 1));
-    const uint32_t sb = lbase + stage * G::kStageBytes;
+  // Fragments of one k-step: B for this wave's column blocks, A for all rows.
+  struct Frags {
     half8 b[G::kColBlocks];
+    half8 a[MB];
+  };
+  auto read_frags = [&](Frags& f, int stage) {
+    const uint32_t sb = lbase + stage * G::kStageBytes;
 #pragma unroll
     for (int c = 0; c < G::kColBlocks; c++) {
       const half4 lo = lds_read_tr16_at(sb + boff[c]);
       const half4 hi = lds_read_tr16_at(sb + boff[c] + 4 * NC * 2);
-      b[c] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      f.b[c] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
-    // All fragment reads go out before the first MFMA (the scheduler by
-    // itself reads A two blocks at a time, each pair waited for).
-    half8 a[MB];
 #pragma unroll
-    for (int r = 0; r < MB; r++) a[r] = lds_read_h8(sb + aoff + r * 1024);
+    for (int r = 0; r < MB; r++) f.a[r] = lds_read_h8(sb + aoff + r * 1024);
+  };
+  // This wave's loads of a step have landed when at most `ahead` later steps
+  // of its loads are still in flight.
+  auto wait_steps = [&](auto ahead) {
+    constexpr int H = decltype(ahead)::value;
+    if (G::kMaxADma == 2 && na == 2)
+      wait_vmcnt<H * (G::kBDma + G::kMaxADma)>();
+    else if (na >= 1)
+      wait_vmcnt<H * (G::kBDma + 1)>();
+    else
+      wait_vmcnt<H * G::kBDma>();
+  };
+
+  // Software pipeline over a ring of S stages: iteration `step` multiplies
+  // the fragments of `step` (read during the previous iteration) while the
+  // fragments of step + 1 are read, so the LDS reads of one k-step overlap
+  // the MFMAs of the one before; the stage of `step` is refilled with step
+  // + S once every wave's reads of it are done (barrier).  Clamped refills
+  // of a short k range land in stages whose contents are never used.
+#pragma unroll
+  for (int st = 0; st < S; st++) issue(st, min(st, nsteps - 1));
+  Frags f[2];
+  wait_steps(std::integral_constant<int, S - 1>{});
+  lds_barrier();
+  read_frags(f[0], 0);
+  auto iteration = [&](int step, Frags& cur, Frags& next) {
+    // This wave's loads of step + 1 landed, then everyone's (barrier); the
+    // barrier also ends every wave's reads of `step`'s stage.
+    wait_steps(std::integral_constant<int, S - 2>{});
+    wait_lgkmcnt0();  // as the barrier's own wait, but visible to the compiler:
+                      // it then knows `cur` has landed and waits for no read
+                      // of `next` before the MFMAs
+    lds_barrier();
+    issue(step % S, min(step + S, nsteps - 1));
+    read_frags(next, (step + 1) % S);
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int r = 0; r < MB; r++)
 #pragma unroll
-      for (int c = 0; c < G::kColBlocks; c++) acc[r][c] = mfma16x16x32(a[r], b[c], acc[r][c]);
+      for (int c = 0; c < G::kColBlocks; c++) acc[r][c] = mfma16x16x32(cur.a[r], cur.b[c], acc[r][c]);
+  };
+  for (int step = 0; step < nsteps; step += 2) {
+    iteration(step, f[0], f[1]);
+    if (step + 1 < nsteps) iteration(step + 1, f[1], f[0]);
   }
   wait_vmcnt<0>();  // clamped tail refills
 
@@ -292,15 +327,12 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
 }
 
 // Workspace: a fixed 4 KB of (column block, wave) counters, then the
-// partials.  K is split only while fewer than 256 column blocks exist
-// (pick_ks), so at most 255 x 4 counters are in use; the counters sit at the
-// same place for every shape, which keeps the library workspace clean (all
-// counters zero) from one call to the next whatever the shapes.  Unsplit
-// shapes need no workspace.
-constexpr size_t kCounterBytes = 4096;
-
-size_t sk_workspace(size_t m, size_t n, size_t k, int) {
-  const int ks = pick_ks(n, k);
+// partials.  K is split only while the counters fit (pick_ks); they sit at
+// the same place for every shape, which keeps the library workspace clean
+// (all counters zero) from one call to the next whatever the shapes.
+// Unsplit shapes need no workspace.
+size_t sk_workspace(size_t m, size_t n, size_t k, int num_cus) {
+  const int ks = pick_ks(n, k, num_cus);
   if (ks == 1) return 0;
   const size_t mb = (m + 15) / 16;
   return kCounterBytes + (size_t)ks * n * 16 * mb * sizeof(float);
@@ -313,7 +345,7 @@ hipError_t launch_sk_t(const GemmArgs& a) {
   auto kfn = f16_skinny_sk_kernel<NC, MB, OutT>;
   hipError_t e = ensure_lds_attr(kfn, G::kLdsBytes, a.device, done);
   if (e != hipSuccess) return e;
-  const int ks = pick_ks(a.n, a.k);
+  const int ks = pick_ks(a.n, a.k, a.num_cus);
   unsigned* counters = nullptr;
   float* part = nullptr;
   if (ks > 1) {
