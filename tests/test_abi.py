@@ -57,6 +57,11 @@ P = 1 << 20  # a 16-byte-aligned fake address: vk_gemm_check never dereferences
     ((1, F16, 7, 256, 256, 256, P, P, P), -2),         # bad dtype code
     ((1, F16, F16, 17, 33, 65, P + 2, P + 4, P + 6), 0),  # v1: any shape, 2-byte aligned
     ((1, F16, F16, 2 ** 31, 1, 1, P, P, P), -8),       # beyond 32-bit indexing
+    ((10, F16, F16, 4000, 4000, 4000, P, P, P), 0),    # v10: any m, n and k multiples of 8
+    ((10, F16, F32, 1, 8, 8, P, P, P), 0),
+    ((10, F16, F16, 4000, 4004, 4000, P, P, P), -3),   # n % 8
+    ((10, F16, F16, 4000, 4000, 4100, P, P, P), -3),   # k % 8
+    ((10, F16, F16, 4000, 4000, 4000, P + 8, P, P), -4),  # 16-byte rows
 ])
 def test_vk_gemm_check(args, expected):
     from vibekernel_amd import _abi
@@ -117,13 +122,15 @@ def test_pick_version_follows_shape():
     assert vk.pick_version(16, 8192, 8192) == 8
     assert vk.pick_version(16, 8224, 8192) == 4  # n % 128 != 0: the 32-column kernel
     assert vk.pick_version(128, 8192, 8192) == 8  # batch-128 decode: still the split-K kernel
-    assert vk.pick_version(144, 8192, 8192) == 1  # beyond 128 rows: the any-shape kernel
+    assert vk.pick_version(144, 8192, 8192) == 10  # beyond 128 rows: v7 with edges
     assert vk.pick_version(4096, 4096, 4096) == 7  # 256 tiles: one full wave
     assert vk.pick_version(4096, 4096, 4096, "f16", "f32") == 7
     assert vk.pick_version(4096, 11008, 4096) == 7  # 688 tiles = 2.69 waves: tail left whole
     assert vk.pick_version(2048, 2048, 4096) == 9   # 64 tiles: split k
     assert vk.pick_version(3840, 4096, 4096) == 7   # 240 of 256 CUs busy: not worth a split
-    assert vk.pick_version(4096, 4096, 4128) == 5  # k % 64 != 0: the 32-deep kernel
+    assert vk.pick_version(4096, 4096, 4128) == 10  # k % 64 != 0: v7 with a masked last k-tile
     assert vk.pick_version(100, 300, 70) == 1
+    assert vk.pick_version(4000, 4000, 4000) == 10  # off the 256 x 256 x 64 grid: v7 with edges
+    assert vk.pick_version(1000, 1000, 1000) == 10
     assert vk.pick_version(512, 512, 512, "f32") == 2   # fp32 on the matrix cores
     assert vk.pick_version(500, 512, 512, "f32") == 1   # m % 256 != 0: the VALU kernel

@@ -1,0 +1,114 @@
+"""GPU parity of version 10 -- version 7's kernel for shapes off its
+256 x 256 x 64 grid (any M; N and K multiples of 8) -- through the C ABI.
+
+* On the grid it runs version 7's arithmetic in version 7's order: bitwise
+  equal results.
+* Ragged shapes (the generic f16 suite adds more): integer inputs exact,
+  random inputs within the fp32 bound of the exact product.
+* Nothing outside C is written: guard regions before and after C keep their
+  NaN poison.
+* What lies past an edge in memory -- the next row of A after k = K, the next
+  row of B after column N -- never reaches a stored element of C: an
+  infinity placed there leaves the other rows and columns finite and exact.
+"""
+import numpy as np
+import pytest
+
+from gpu_util import announce, check_f16_out, check_f32_out, make_inputs, run_gemm
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("shape", [(256, 256, 64), (512, 768, 320), (1024, 512, 1024)])
+@pytest.mark.parametrize("out", ["f16", "f32"])
+def test_on_grid_equals_v7(gpu, shape, out):
+    m, n, k = shape
+    A, B = make_inputs(m, n, k, "normal", seed=m + n + k)
+    C7 = run_gemm(7, A, B, out)
+    C10 = run_gemm(10, A, B, out)
+    assert np.array_equal(C7.view(np.uint16 if out == "f16" else np.uint32),
+                          C10.view(np.uint16 if out == "f16" else np.uint32))
+
+
+@pytest.mark.parametrize("shape", [(300, 264, 72), (1, 8, 8), (257, 1000, 512), (600, 40, 1032)])
+@pytest.mark.parametrize("out", ["f16", "f32"])
+def test_writes_only_c(gpu, shape, out):
+    """C sits between two 4096-element guard regions of NaN; integer inputs
+    in [-2, 2] with k <= 1032 keep every sum exact in fp32 and, up to 2048,
+    in fp16."""
+    import torch
+    import vibekernel_amd as vk
+    m, n, k = shape
+    A, B = make_inputs(m, n, k, "int", seed=m * 7 + n + k)
+    exact = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.int64)
+    if out == "f16" and np.abs(exact).max() > 2048:
+        pytest.skip("integer result not exact in fp16")
+    pad = 4096
+    dt = torch.float16 if out == "f16" else torch.float32
+    buf = torch.full((pad + m * n + pad,), float("nan"), dtype=dt, device="cuda:0")
+    C = buf[pad:pad + m * n].view(m, n)
+    announce(f"version=10 guarded m={m} n={n} k={k} out={out}")
+    vk.matmul(m, n, k, torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda(), C, 10)
+    torch.cuda.synchronize()
+    assert torch.isnan(buf[:pad]).all() and torch.isnan(buf[pad + m * n:]).all()
+    assert np.array_equal(C.cpu().numpy().astype(np.int64), exact)
+
+
+@pytest.mark.parametrize("out", ["f16", "f32"])
+def test_values_past_the_edges_never_reach_c(gpu, out):
+    """M = 3, N = 8, K = 72: row 0's last k-tile covers k = 64..127, and
+    k = 72..79 of row 0 is, in memory, A[1][0..7]; columns 8..15 of B's row r
+    are B[r+1][0..7].  With A[1][0] and B[5][0] infinite, row 1 and column 0
+    of C are not finite, and everything else must equal the exact product."""
+    m, n, k = 3, 8, 72
+    A, B = make_inputs(m, n, k, "int", seed=72)
+    A[1, 0] = np.inf
+    B[5, 0] = np.inf
+    C = run_gemm(10, A, B, out).astype(np.float64)
+    with np.errstate(invalid="ignore"):
+        exact = A.astype(np.float64) @ B.astype(np.float64)
+    keep = np.ones((m, n), dtype=bool)
+    keep[1, :] = False
+    keep[:, 0] = False
+    assert np.all(np.isfinite(C[keep]))
+    assert np.array_equal(C[keep], exact[keep])
+
+
+@pytest.mark.parametrize("shape", [(1000, 1000, 1000), (4096, 4096, 4128), (2000, 3000, 1000)])
+def test_ragged_random_vs_oracle(gpu, oracle, shape):
+    m, n, k = shape
+    A, B = make_inputs(m, n, k, "uniform", seed=10 + m + k)
+    C64 = oracle.dgemm(A, B)
+    check_f32_out(run_gemm(10, A, B, "f32"), A, B, C64)
+    C16 = run_gemm(10, A, B, "f16")
+    check_f16_out(C16, A, B, C64)
+    err, st = oracle.mean_rel_err(oracle.hgemm(A, B), C16)
+    assert st == oracle.STATUS_OK and err < 2e-4
+
+
+@pytest.mark.slow
+def test_4000_cubed(gpu, oracle):
+    m = n = k = 4000
+    A, B = make_inputs(m, n, k, "uniform", seed=4000)
+    C64 = oracle.dgemm(A, B)
+    check_f16_out(run_gemm(10, A, B, "f16"), A, B, C64)
+
+
+@pytest.mark.slow
+def test_edge_repeat_deterministic(gpu):
+    """110 launches with C poisoned before each: bitwise equal."""
+    import torch
+    import vibekernel_amd as vk
+    m, n, k = 1000, 1000, 1000
+    g = torch.Generator(device="cuda:0").manual_seed(10)
+    A = (torch.rand((m, k), generator=g, device="cuda:0") * 2 - 1).half()
+    B = (torch.rand((k, n), generator=g, device="cuda:0") * 2 - 1).half()
+    C = torch.empty((m, n), dtype=torch.float16, device="cuda:0")
+    announce(f"version=10 repeat x110 {m}x{n}x{k}")
+    vk.matmul(m, n, k, A, B, C, 10)
+    ref = C.clone()
+    for _ in range(110):
+        C.fill_(float("nan"))
+        vk.matmul(m, n, k, A, B, C, 10)
+        assert torch.equal(C, ref)
+    torch.cuda.synchronize()

@@ -18,6 +18,7 @@ pytestmark = pytest.mark.gpu
 
 TILE_SHAPES = [(256, 256, 64), (512, 256, 128), (256, 512, 192), (768, 512, 256), (1024, 1024, 512)]
 ANY_SHAPES = [(1, 1, 1), (17, 33, 65), (127, 129, 31), (200, 300, 100), (256, 256, 64), (64, 8, 1000)]
+EDGE_SHAPES = [(1, 8, 8), (17, 40, 72), (100, 264, 136), (255, 256, 64), (257, 520, 200), (300, 1000, 520)]
 SKINNY_SHAPES = [(16, 256, 512), (32, 512, 1024), (48, 96, 128), (64, 128, 256), (16, 2048, 4096),
                  (80, 256, 512), (96, 384, 96), (112, 128, 1024), (128, 1024, 2048)]
 
@@ -33,6 +34,8 @@ def _shapes_for(version):
     shapes = [s for s in TILE_SHAPES if s[0] % c.div_m == 0 and s[1] % c.div_n == 0 and s[2] % c.div_k == 0]
     if c.div_m == 1 and c.div_n == 1 and c.div_k == 1:
         shapes = ANY_SHAPES + shapes[:2]
+    elif c.div_m == 1:
+        shapes = EDGE_SHAPES + shapes[:2]
     if c.max_m <= 128:
         shapes = [s for s in SKINNY_SHAPES if s[0] <= c.max_m and s[0] % c.div_m == 0
                   and s[1] % c.div_n == 0 and s[2] % c.div_k == 0]

@@ -582,6 +582,20 @@ struct Epi16<half_t> {
       *reinterpret_cast<uint4v*>(Cw + (size_t)row * N + ch * 8) = v;
     }
   }
+  // The same for a block at (row0, col0) of C that may reach past M rows or
+  // N columns (N a multiple of 8): chunks outside are not stored.
+  static __device__ __forceinline__ void flush_edge(uint32_t wbase, half_t* C, int M, int N, int row0, int col0,
+                                                    int lane, int half) {
+    if (half == 0) return;
+    const int rsub = lane >> 3, ch = lane & 7;
+    const bool col_in = col0 + ch * 8 < N;
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+      const int row = 8 * q + rsub;
+      const uint4v v = lds_read16(epi16_addr(wbase, row, ch));
+      if (col_in && row0 + row < M) *reinterpret_cast<uint4v*>(C + (size_t)(row0 + row) * N + col0 + ch * 8) = v;
+    }
+  }
 };
 
 // fp32: 64 rows per half (row pitch 256 B = 16 chunks, physical chunk =
@@ -603,6 +617,19 @@ struct Epi16<float> {
     }
     if (half == 0) wait_lgkmcnt0();  // the region is rewritten by the second half
   }
+  static __device__ __forceinline__ void flush_edge(uint32_t wbase, float* C, int M, int N, int row0, int col0,
+                                                    int lane, int half) {
+    const int rsub = lane >> 4, ch = lane & 15;
+    const bool col_in = col0 + ch * 4 < N;
+#pragma unroll
+    for (int q = 0; q < 16; q++) {
+      const int row = 4 * q + rsub;
+      const uint4v v = lds_read16(wbase + row * 256 + 16 * (ch ^ (row & 15)));
+      const int r = row0 + half * 64 + row;
+      if (col_in && r < M) *reinterpret_cast<uint4v*>(C + (size_t)r * N + col0 + ch * 4) = v;
+    }
+    if (half == 0) wait_lgkmcnt0();
+  }
 };
 
 template <typename OutT>
@@ -617,13 +644,29 @@ __device__ __forceinline__ void epilogue16(float4v (&acc)[8][4], uint32_t wbase,
   }
 }
 
+template <typename OutT>
+__device__ __forceinline__ void epilogue16_edge(float4v (&acc)[8][4], uint32_t wbase, OutT* C, int M, int N,
+                                                int row0, int col0, int lane) {
+#pragma unroll
+  for (int half = 0; half < 2; half++) {
+#pragma unroll
+    for (int i = 4 * half; i < 4 * half + 4; i++)
+#pragma unroll
+      for (int j = 0; j < 4; j++) Epi16<OutT>::stage(wbase, lane, i, j, acc[i][j]);
+    Epi16<OutT>::flush_edge(wbase, C, M, N, row0, col0, lane, half);
+  }
+}
+
 // The k-loop of one 256x256 tile over k-tiles kb .. kb + nk - 1 (nk >= 1):
 // zeroes `acc`, runs the prologue, the two-phase loop and the closing
 // barriers, and leaves the wave's 128x64 block of C in `acc` with the LDS ring
-// idle.  A and B point at the whole matrices; m0, n0 name the tile.
+// idle.  A and B point at the whole matrices; m0, n0 name the tile.  kEdge
+// (version 10): the tile may reach past M rows, N columns or K (M any; N, K
+// multiples of 8); what lies outside the matrices is loaded as zeros.
+template <bool kEdge = false>
 __device__ __forceinline__ void pp16_mainloop(const half_t* __restrict__ A, const half_t* __restrict__ B, int N,
                                               int K, int m0, int n0, int kb, int nk, uint32_t lds_base, int grp,
-                                              int gw, int lane, float4v (&acc)[8][4]) {
+                                              int gw, int lane, float4v (&acc)[8][4], int M = 0) {
   // ---- direct-to-LDS duty: instruction d = 4h + i (8 per wave per k-tile) ----
   // Q, A: rows gw*32 + 8i .. +7 of the A-top (h = 0) or A-bot (h = 1) half,
   //   landing at half offset (gw*4 + i) * 1024.
@@ -652,11 +695,46 @@ __device__ __forceinline__ void pp16_mainloop(const half_t* __restrict__ A, cons
   const uint32_t l_slot = grp ? (uint32_t)kHalfBytes : (uint32_t)kBBytes;  // per slot
   const uint32_t l_h = grp ? (uint32_t)(kABot - kATop) : 4u * 512u;       // per h
 
+  // Edges: the same loads through a buffer resource over the whole matrix
+  // (each operand below 2^31 bytes), the k-tile's offset from the matrix
+  // start in the scalar offset and the lane's within the k-tile as before,
+  // so a lane past the end of the matrix reads zeros: A rows at or below M,
+  // B k-rows at or below K.  B columns past N (in range: the next row's) only
+  // feed C columns that are not stored.  What remains is A's k past K on the
+  // last k-tile (the next row's values, which must not meet B's zero rows:
+  // an infinity there would make a NaN): such lanes get the matrix size as
+  // their offset.  Bits 6i..6i+5 of akin: the first k of the lane's A chunk
+  // of instruction i within a k-tile (a select, not a branch, inside the
+  // MFMA sequence: a branch there made the fp32-output kernel spill).
+  uint32_t akin = 0;
+  if constexpr (kEdge) {
+    if (grp) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int row = gw * 32 + i * 8 + (lane >> 3);
+        akin |= (uint32_t)(((lane & 7) ^ swz_a16(row)) * 8) << (6 * i);
+      }
+    }
+  }
+  const char* g_start = grp ? reinterpret_cast<const char*>(A) : reinterpret_cast<const char*>(B);
+  const uint32_t g_size = kEdge ? (uint32_t)(grp ? M * K * 2 : K * N * 2) : 0u;
+  const __amdgpu_buffer_rsrc_t g_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(g_start), 0, (int)g_size, kBufferWord3);
+  const uint32_t g_off0 = (uint32_t)(g_base - g_start);  // the tile's first k-tile (kEdge: below 2^31)
+
   auto dma = [&](int d, int kt, int slot) {
     const int i = d & 3, h = d >> 2;
     const uint32_t l_i = grp ? (uint32_t)i * 1024 : (uint32_t)((i & 1) * 1024 + (i >> 1) * 4096);
-    const char* gp = g_base + (size_t)kt * g_kt + h * g_h;
-    dma16(gp, voff[i], l_base + slot * l_slot + h * l_h + l_i);
+    const uint32_t ldst = l_base + slot * l_slot + h * l_h + l_i;
+    if constexpr (kEdge) {
+      const uint32_t soff = g_off0 + (uint32_t)kt * (uint32_t)g_kt + (uint32_t)h * (uint32_t)g_h;
+      // k from this k-tile's start to K (> 0); B's lanes are never masked here
+      const uint32_t kleft = grp ? (uint32_t)(K - (kb + kt) * kBK) : 64u;
+      const uint32_t off = ((akin >> (6 * i)) & 63u) < kleft ? voff[i] : g_size;  // g_size: zeros
+      dma16_buf(g_rsrc, off, soff, ldst);
+    } else {
+      dma16(g_base + (size_t)kt * g_kt + h * g_h, voff[i], ldst);
+    }
   };
 
   // ---- fragment addresses ----
@@ -807,6 +885,59 @@ hipError_t launch_t(const GemmArgs& a) {
 
 hipError_t launch(const GemmArgs& a) {
   return a.out_dtype == VK_DTYPE_F16 ? launch_t<half_t>(a) : launch_t<float>(a);
+}
+
+// ---------------------------------------------------------------------------
+// Version 10: version 7 for shapes off its 256 x 256 x 64 grid -- any M, N and
+// K multiples of 8 (16-byte rows).  Same tiles, schedule and kernel body; the
+// tiles on the right and bottom edges and the last k-tile reach past the
+// matrices: their loads go through buffer resources that return zeros past
+// the end of a matrix, the A chunks past K are masked, and the C stores skip
+// the chunks outside.  The reference's kernels would launch no blocks for
+// such shapes (matmul_f16_v42_shfl2.cu:124, :520-527).
+template <typename OutT>
+__global__ __launch_bounds__(kThreads) void f16_pp16_edge_kernel(const half_t* __restrict__ A,
+                                                                 const half_t* __restrict__ B,
+                                                                 OutT* __restrict__ C, int M, int N, int K) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;
+  const int gw = wave & 3;
+
+  int tm, tn;
+  tile_of(blockIdx.x, (M + kBM - 1) / kBM, (N + kBN - 1) / kBN, tm, tn);
+  const int m0 = tm * kBM, n0 = tn * kBN;
+  const uint32_t lds_base = lds_addr32(lds);
+
+  float4v acc[8][4];
+  pp16_mainloop<true>(A, B, N, K, m0, n0, 0, (K + kBK - 1) / kBK, lds_base, grp, gw, lane, acc, M);
+  epilogue16_edge<OutT>(acc, lds_base + wave * (128 * 64 * 2), C, M, N, m0 + grp * 128, n0 + gw * 64,
+                        lane_from_exec());
+}
+
+template <typename OutT>
+hipError_t launch_edge_t(const GemmArgs& a) {
+  static std::atomic<uint64_t> attr_done{0};
+  auto kfn = f16_pp16_edge_kernel<OutT>;
+  hipError_t e = ensure_lds_attr(kfn, kLdsBytes, a.device, attr_done);
+  if (e != hipSuccess) return e;
+  const int tiles = (int)(((a.m + kBM - 1) / kBM) * ((a.n + kBN - 1) / kBN));
+  hipLaunchKernelGGL(kfn, dim3(tiles), dim3(kThreads), kLdsBytes, a.stream,
+                     static_cast<const half_t*>(a.A), static_cast<const half_t*>(a.B),
+                     static_cast<OutT*>(a.C), (int)a.m, (int)a.n, (int)a.k);
+  return hipGetLastError();
+}
+
+hipError_t launch_edge(const GemmArgs& a) {
+  return a.out_dtype == VK_DTYPE_F16 ? launch_edge_t<half_t>(a) : launch_edge_t<float>(a);
+}
+
+// Each operand below 2^31 bytes (buffer sizes), and version 7's 32-bit lane
+// offsets (128 rows of A, 64 k-rows of B) and tile count.
+bool edge_shape_ok(size_t m, size_t n, size_t k) {
+  return m >= 1 && n >= 8 && k >= 8 && m * k * 2 < (1ull << 31) && k * n * 2 < (1ull << 31) &&
+         pp64::shape_ok(((m + kBM - 1) / kBM) * kBM, ((n + kBN - 1) / kBN) * kBN, k);
 }
 
 // ---------------------------------------------------------------------------
@@ -1000,6 +1131,15 @@ void register_f16_pingpong() {
   e7.caps.version = 7;
   e7.launch = pp16::launch;
   register_kernel(e7);
+
+  KernelEntry e10 = e7;
+  e10.version = 10;
+  e10.name = "f16_v10_pp256_edge";
+  e10.caps = make_caps(10, VK_DTYPE_F16, kOutF16 | kOutF32, 1, 8, 8, 16, kBM, kBN, pp64::kBK, kThreads,
+                       pp64::kLdsBytes, 0, 0);
+  e10.launch = pp16::launch_edge;
+  e10.shape_ok = pp16::edge_shape_ok;
+  register_kernel(e10);
 
   KernelEntry e9 = e7;
   e9.version = 9;

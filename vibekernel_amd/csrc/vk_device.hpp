@@ -173,6 +173,17 @@ __device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t
                : "s"(lds_dst), "v"(voff), "s"(gbase)
                : "m0");
 }
+// The same through a buffer resource, lane l's 16 bytes at soff + voff of
+// it: a lane whose bytes are not below the resource's size reads zeros and
+// touches no memory (the wave-uniform soff counts in that test: measured on
+// MI355X), which is how a lane outside a matrix is masked.
+__device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff,
+                                          uint32_t lds_dst) {
+  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+               :
+               : "s"(lds_dst), "v"(voff), "s"(rsrc), "s"(soff)
+               : "m0");
+}
 #pragma clang diagnostic pop
 
 // An inline-asm operand in an AGPR marks the kernel as using AGPRs, and the

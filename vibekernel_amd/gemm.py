@@ -96,15 +96,17 @@ def query(version: int, dtype: str = "f16"):
 def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = None) -> int:
     """The fastest version that accepts this shape (checked with vk_gemm_check
     on 4 KiB-aligned placeholder addresses; nothing is launched): for fp16
-    the skinny kernels when M <= 128 (64 for version 4), then the 256x256 kernels (fastest first), then
-    the any-shape kernel.  The split-tail version 9 comes first among the 256x256
-    kernels only where its schedule splits tiles on this device (it then needs
-    a workspace); elsewhere it would run version 7's whole tiles.  The
-    reference picks versions at build time only (CMakeLists.txt
-    MATMUL_VERSION); this is a convenience of the front end."""
+    the skinny kernels when M <= 128 (64 for version 4), then the 256x256
+    kernels (fastest first; version 10 takes shapes off the 256 x 256 x 64
+    grid whose N and K are multiples of 8), then the any-shape kernel.  The
+    split-tail version 9 comes first among the 256x256 kernels only where its
+    schedule splits tiles on this device (it then needs a workspace);
+    elsewhere it would run version 7's whole tiles.  The reference picks
+    versions at build time only (CMakeLists.txt MATMUL_VERSION); this is a
+    convenience of the front end."""
     in_dt = DTYPE_F16 if dtype == "f16" else DTYPE_F32
     out_dt = DTYPE_F16 if (out or dtype) == "f16" else DTYPE_F32
-    order = [8, 4, 9, 7, 6, 5, 3, 2, 1] if in_dt == DTYPE_F16 else [2, 1]
+    order = [8, 4, 9, 7, 10, 6, 5, 3, 2, 1] if in_dt == DTYPE_F16 else [2, 1]
     avail = set(_abi.versions(in_dt))
     for v in order:
         if v == 9 and _abi.workspace_bytes(v, in_dt, m, n, k) == 0:
