@@ -109,6 +109,18 @@ def test_splittail_workspace_follows_schedule():
     assert _abi.workspace_bytes(9, f16, 256, 256, 512) == 0        # 8 k-tiles: too shallow to split
 
 
+def test_edge_split_plan_follows_shape():
+    """Version 10 takes version 9's split tails where the plan splits, with
+    the tiles and k-tiles past M, N or K counted whole."""
+    from vibekernel_amd import _abi
+    f16 = _abi.DTYPE_F16
+    assert _abi.query(10, f16).uses_workspace == 1
+    assert _abi.workspace_bytes(10, f16, 4000, 4000, 4000) == 0   # 256 tiles: one full wave
+    assert _abi.workspace_bytes(10, f16, 1000, 1000, 1000) == 0   # 16 k-tiles: too shallow to split
+    assert _abi.workspace_bytes(10, f16, 1000, 1000, 4000) == 8192 + 64 * 256 * 1024  # 16 tiles x 4 pieces
+    assert _abi.workspace_bytes(10, f16, 4096, 4096, 4096) == 0
+
+
 def test_single_hip_runtime_in_process():
     """The library must bind to the HIP runtime the process already uses
     (PyTorch's), never map a second one."""

@@ -7,6 +7,9 @@
   random inputs within the fp32 bound of the exact product.
 * Nothing outside C is written: guard regions before and after C keep their
   NaN poison.
+* Where its split-tail plan splits (a part-empty last wave, e.g. 1000 x
+  1000 x 4000 = 16 tiles), the pieces of a tile meet through the workspace
+  as in version 9: same bars, bitwise repeatable, a caller workspace works.
 * What lies past an edge in memory -- the next row of A after k = K, the next
   row of B after column N -- never reaches a stored element of C: an
   infinity placed there leaves the other rows and columns finite and exact.
@@ -30,7 +33,7 @@ def test_on_grid_equals_v7(gpu, shape, out):
                           C10.view(np.uint16 if out == "f16" else np.uint32))
 
 
-@pytest.mark.parametrize("shape", [(300, 264, 72), (1, 8, 8), (257, 1000, 512), (600, 40, 1032)])
+@pytest.mark.parametrize("shape", [(300, 264, 72), (1, 8, 8), (257, 1000, 512), (600, 40, 1032), (257, 520, 4096)])
 @pytest.mark.parametrize("out", ["f16", "f32"])
 def test_writes_only_c(gpu, shape, out):
     """C sits between two 4096-element guard regions of NaN; integer inputs
@@ -74,7 +77,8 @@ def test_values_past_the_edges_never_reach_c(gpu, out):
     assert np.array_equal(C[keep], exact[keep])
 
 
-@pytest.mark.parametrize("shape", [(1000, 1000, 1000), (4096, 4096, 4128), (2000, 3000, 1000)])
+@pytest.mark.parametrize("shape", [(1000, 1000, 1000), (4096, 4096, 4128), (2000, 3000, 1000), (1000, 1000, 4000),
+                                   (257, 520, 4096), (1496, 1496, 3000)])
 def test_ragged_random_vs_oracle(gpu, oracle, shape):
     m, n, k = shape
     A, B = make_inputs(m, n, k, "uniform", seed=10 + m + k)
@@ -99,7 +103,7 @@ def test_edge_repeat_deterministic(gpu):
     """110 launches with C poisoned before each: bitwise equal."""
     import torch
     import vibekernel_amd as vk
-    m, n, k = 1000, 1000, 1000
+    m, n, k = 1000, 1000, 4000  # split tail: 16 tiles in k-slices
     g = torch.Generator(device="cuda:0").manual_seed(10)
     A = (torch.rand((m, k), generator=g, device="cuda:0") * 2 - 1).half()
     B = (torch.rand((k, n), generator=g, device="cuda:0") * 2 - 1).half()
@@ -112,3 +116,27 @@ def test_edge_repeat_deterministic(gpu):
         vk.matmul(m, n, k, A, B, C, 10)
         assert torch.equal(C, ref)
     torch.cuda.synchronize()
+
+
+def test_split_caller_workspace(gpu):
+    """vk_gemm_ws with a caller workspace full of garbage on a split shape:
+    the launch clears the counters it keeps there, so the result equals the
+    library-workspace call, call after call."""
+    import torch
+    from vibekernel_amd import _abi
+    m, n, k = 257, 520, 4096
+    A, B = make_inputs(m, n, k, "uniform", seed=257)
+    ref = run_gemm(10, A, B, "f32")
+    need = _abi.workspace_bytes(10, _abi.DTYPE_F16, m, n, k)
+    assert need > 0
+    ws = torch.full((need // 4 + 64,), -1, dtype=torch.int32, device="cuda:0")
+    tA = torch.from_numpy(A).cuda()
+    tB = torch.from_numpy(B).cuda()
+    for _ in range(3):
+        tC = torch.full((m, n), float("nan"), dtype=torch.float32, device="cuda:0")
+        announce(f"version=10 caller workspace m={m} n={n} k={k}")
+        st = _abi.gemm_ws(10, _abi.DTYPE_F16, _abi.DTYPE_F32, m, n, k, tA.data_ptr(), tB.data_ptr(),
+                          tC.data_ptr(), ws.data_ptr(), ws.numel() * 4)
+        assert st == 0
+        torch.cuda.synchronize()
+        assert np.array_equal(tC.cpu().numpy(), ref)

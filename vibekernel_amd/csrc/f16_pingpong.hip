@@ -993,10 +993,12 @@ __device__ __forceinline__ bool sk_arrive(float4v (&acc)[8][4], int np, int p, _
 
 // Store of the wave's block of C: acc alone for a whole tile (np = 1); for a
 // split tile, the last arrival's sum of all pieces, after which the counter is
-// reset for the next call.
-template <typename OutT, typename PartOff>
+// reset for the next call.  The block starts at row row0, column col0 of C;
+// kEdge: it may reach past M rows or N columns, which are not stored.
+template <typename OutT, bool kEdge, typename PartOff>
 __device__ __forceinline__ void sk_write_c(float4v (&acc)[8][4], int np, int p, __amdgpu_buffer_rsrc_t part,
-                                           PartOff part_off, unsigned* cnt, uint32_t wstage, OutT* Cw, int N) {
+                                           PartOff part_off, unsigned* cnt, uint32_t wstage, OutT* C, int M,
+                                           int N, int row0, int col0) {
   const int lane = lane_from_exec();
   const uint32_t vlane = (uint32_t)lane * 16;
   // The counter read that made this wave the last stays before the reads of
@@ -1029,12 +1031,15 @@ __device__ __forceinline__ void sk_write_c(float4v (&acc)[8][4], int np, int p, 
 #pragma unroll
       for (int b = 0; b < 8; b++) Epi16<OutT>::stage(wstage, lane, 2 * bb + (b >> 2), b & 3, t[b]);
     }
-    Epi16<OutT>::flush(wstage, Cw, N, lane, half);
+    if constexpr (kEdge)
+      Epi16<OutT>::flush_edge(wstage, C, M, N, row0, col0, lane, half);
+    else
+      Epi16<OutT>::flush(wstage, C + (size_t)row0 * N + col0, N, lane, half);
   }
   if (np > 1 && lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-template <typename OutT>
+template <typename OutT, bool kEdge>
 __global__ __launch_bounds__(kThreads) void f16_pp16_sk_kernel(const half_t* __restrict__ A,
                                                                const half_t* __restrict__ B,
                                                                OutT* __restrict__ C, int M, int N, int K, int dp,
@@ -1046,8 +1051,11 @@ __global__ __launch_bounds__(kThreads) void f16_pp16_sk_kernel(const half_t* __r
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = wave >> 2;
   const int gw = wave & 3;
-  const int tiles_m = M / kBM, tiles_n = N / kBN, T = tiles_m * tiles_n;
-  const int I = K / kBK;
+  // kEdge (version 10's split tails): the tiles and k-tiles that reach past
+  // M, N or K count as whole ones, as in f16_pp16_edge_kernel.
+  const int tiles_m = (M + (kEdge ? kBM - 1 : 0)) / kBM, tiles_n = (N + (kEdge ? kBN - 1 : 0)) / kBN;
+  const int T = tiles_m * tiles_n;
+  const int I = (K + (kEdge ? kBK - 1 : 0)) / kBK;
   const uint32_t lds_base = lds_addr32(lds);
   const uint32_t wstage = lds_base + wave * (128 * 64 * 2);
   const int bid = blockIdx.x;
@@ -1058,8 +1066,7 @@ __global__ __launch_bounds__(kThreads) void f16_pp16_sk_kernel(const half_t* __r
   raster_tile(w.cid, tiles_m, tiles_n, tm, tn);
   const int m0 = tm * kBM, n0 = tn * kBN;
   float4v acc[8][4];
-  pp16_mainloop(A, B, N, K, m0, n0, w.kb, w.ke - w.kb, lds_base, grp, gw, lane, acc);
-  OutT* Cw = C + (size_t)(m0 + grp * 128) * N + n0 + gw * 64;
+  pp16_mainloop<kEdge>(A, B, N, K, m0, n0, w.kb, w.ke - w.kb, lds_base, grp, gw, lane, acc, M);
   // One partial slot per split-tail unit (at most 256: 64 MB, within 32-bit
   // offsets); piece q of this tile is in the slot of unit sk_unit_of(.., q).
   const __amdgpu_buffer_rsrc_t prsrc =
@@ -1069,16 +1076,24 @@ __global__ __launch_bounds__(kThreads) void f16_pp16_sk_kernel(const half_t* __r
   };
   unsigned* cnt = counters + (size_t)w.tile * kSkWaves + wave;
   if (w.np == 1 || sk_arrive(acc, w.np, w.p, prsrc, part_off, cnt))
-    sk_write_c<OutT>(acc, w.np, w.p, prsrc, part_off, cnt, wstage, Cw, N);
+    sk_write_c<OutT, kEdge>(acc, w.np, w.p, prsrc, part_off, cnt, wstage, C, M, N, m0 + grp * 128, n0 + gw * 64);
 }
 
-template <typename OutT>
+// Split-tail plan of a shape: kEdge counts the tiles and k-tiles that reach
+// past M, N or K.
+template <bool kEdge>
+SkPlan sk_plan_of(size_t m, size_t n, size_t k, int num_cus) {
+  const size_t tm = kEdge ? (m + kBM - 1) / kBM : m / kBM, tn = kEdge ? (n + kBN - 1) / kBN : n / kBN;
+  return sk_plan((int64_t)(tm * tn), (int64_t)(kEdge ? (k + kBK - 1) / kBK : k / kBK), num_cus);
+}
+
+template <typename OutT, bool kEdge>
 hipError_t launch_sk_t(const GemmArgs& a) {
   static std::atomic<uint64_t> attr_done{0};
-  auto kfn = f16_pp16_sk_kernel<OutT>;
+  auto kfn = f16_pp16_sk_kernel<OutT, kEdge>;
   hipError_t e = ensure_lds_attr(kfn, kLdsBytes, a.device, attr_done);
   if (e != hipSuccess) return e;
-  const SkPlan p = sk_plan((int64_t)((a.m / kBM) * (a.n / kBN)), (int64_t)(a.k / kBK), a.num_cus);
+  const SkPlan p = sk_plan_of<kEdge>(a.m, a.n, a.k, a.num_cus);
   unsigned* counters = nullptr;
   float* part = nullptr;
   if (p.units > 0) {
@@ -1096,7 +1111,20 @@ hipError_t launch_sk_t(const GemmArgs& a) {
 }
 
 hipError_t launch_sk(const GemmArgs& a) {
-  return a.out_dtype == VK_DTYPE_F16 ? launch_sk_t<half_t>(a) : launch_sk_t<float>(a);
+  return a.out_dtype == VK_DTYPE_F16 ? launch_sk_t<half_t, false>(a) : launch_sk_t<float, false>(a);
+}
+
+// Version 10: whole tiles with masked edges, or, where the split-tail plan
+// splits (a part-empty last wave, e.g. 1000^3 = 16 tiles), version 9's
+// schedule with the same edges.
+hipError_t launch_edge_any(const GemmArgs& a) {
+  if (sk_plan_of<true>(a.m, a.n, a.k, a.num_cus).units == 0) return launch_edge(a);
+  return a.out_dtype == VK_DTYPE_F16 ? launch_sk_t<half_t, true>(a) : launch_sk_t<float, true>(a);
+}
+
+size_t sk_workspace_edge(size_t m, size_t n, size_t k, int num_cus) {
+  const SkPlan p = sk_plan_of<true>(m, n, k, num_cus);
+  return p.units ? kSkCounterBytes + (size_t)p.units * kSkSlotBytes : 0;
 }
 
 }  // namespace pp16
@@ -1137,7 +1165,9 @@ void register_f16_pingpong() {
   e10.name = "f16_v10_pp256_edge";
   e10.caps = make_caps(10, VK_DTYPE_F16, kOutF16 | kOutF32, 1, 8, 8, 16, kBM, kBN, pp64::kBK, kThreads,
                        pp64::kLdsBytes, 0, 0);
-  e10.launch = pp16::launch_edge;
+  e10.caps.uses_workspace = 1;
+  e10.launch = pp16::launch_edge_any;
+  e10.workspace = pp16::sk_workspace_edge;
   e10.shape_ok = pp16::edge_shape_ok;
   register_kernel(e10);
 
