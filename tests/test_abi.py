@@ -62,6 +62,8 @@ P = 1 << 20  # a 16-byte-aligned fake address: vk_gemm_check never dereferences
     ((10, F16, F16, 4000, 4004, 4000, P, P, P), -3),   # n % 8
     ((10, F16, F16, 4000, 4000, 4100, P, P, P), -3),   # k % 8
     ((10, F16, F16, 4000, 4000, 4000, P + 8, P, P), -4),  # 16-byte rows
+    ((3, F32, F32, 1000, 1000, 1000, P, P, P), 0),     # f32 v3: any m, n and k multiples of 4
+    ((3, F32, F32, 1000, 1002, 1000, P, P, P), -3),
 ])
 def test_vk_gemm_check(args, expected):
     from vibekernel_amd import _abi
@@ -145,4 +147,5 @@ def test_pick_version_follows_shape():
     assert vk.pick_version(4000, 4000, 4000) == 10  # off the 256 x 256 x 64 grid: v7 with edges
     assert vk.pick_version(1000, 1000, 1000) == 10
     assert vk.pick_version(512, 512, 512, "f32") == 2   # fp32 on the matrix cores
-    assert vk.pick_version(500, 512, 512, "f32") == 1   # m % 256 != 0: the VALU kernel
+    assert vk.pick_version(500, 512, 512, "f32") == 3   # m % 256 != 0: the matrix cores with edges
+    assert vk.pick_version(500, 510, 512, "f32") == 1   # n % 4 != 0: the VALU kernel

@@ -5,7 +5,10 @@
   bit for bit, on every shape;
 * version 2 (matrix cores, v_mfma_f32_32x32x2_f32, two products per step):
   integer inputs exact; random inputs within 2 k u |A||B| of the exact
-  (fp64) product; bitwise repeatable launch to launch.
+  (fp64) product; bitwise repeatable launch to launch;
+* version 3 (version 2 with masked edges: any M, N and K multiples of 4): the
+  same bars on ragged shapes, bitwise equal to version 2 on its grid, nothing
+  written outside C, and the values past an edge in memory never reach C.
 """
 import numpy as np
 import pytest
@@ -16,7 +19,8 @@ pytestmark = pytest.mark.gpu
 
 SHAPES_V1 = [(128, 128, 16), (256, 384, 64), (512, 512, 512), (1, 1, 1), (17, 33, 65), (130, 250, 70)]
 SHAPES_V2 = [(256, 256, 16), (512, 256, 64), (256, 512, 48), (768, 512, 256), (1024, 1024, 512)]
-CASES = [(1, s) for s in SHAPES_V1] + [(2, s) for s in SHAPES_V2]
+SHAPES_V3 = [(1, 4, 4), (17, 36, 68), (300, 260, 100), (257, 512, 36), (1000, 1000, 1000), (256, 256, 64)]
+CASES = [(1, s) for s in SHAPES_V1] + [(2, s) for s in SHAPES_V2] + [(3, s) for s in SHAPES_V3]
 
 
 def _run(A, B, version):
@@ -104,3 +108,45 @@ def test_f32_mfma_rejects_unaligned_shape(gpu):
     with pytest.raises(vk.VkError) as e:
         vk.matmul(500, 256, 64, A, B, C, 2)
     assert e.value.status == -3
+
+
+def test_f32_edge_on_grid_equals_v2(gpu):
+    """On version 2's grid with K % 32 == 0 both run 32-deep k-tiles in the
+    same order: bitwise equal."""
+    for m, n, k in [(256, 256, 64), (512, 768, 320)]:
+        A, B = make_inputs(m, n, k, "normal", seed=m + k, dtype=np.float32)
+        assert np.array_equal(_run(A, B, 2).view(np.uint32), _run(A, B, 3).view(np.uint32))
+
+
+@pytest.mark.parametrize("shape", [(300, 260, 100), (1, 4, 4), (600, 36, 1028)])
+def test_f32_edge_writes_only_c(gpu, shape):
+    import torch
+    import vibekernel_amd as vk
+    m, n, k = shape
+    A, B = make_inputs(m, n, k, "int", seed=m + n, dtype=np.float32)
+    pad = 4096
+    buf = torch.full((pad + m * n + pad,), float("nan"), dtype=torch.float32, device="cuda:0")
+    C = buf[pad:pad + m * n].view(m, n)
+    announce(f"f32 version=3 guarded m={m} n={n} k={k}")
+    vk.matmul(m, n, k, torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda(), C, 3)
+    torch.cuda.synchronize()
+    assert torch.isnan(buf[:pad]).all() and torch.isnan(buf[pad + m * n:]).all()
+    exact = (A.astype(np.float64) @ B.astype(np.float64)).astype(np.int64)
+    assert np.array_equal(C.cpu().numpy().astype(np.int64), exact)
+
+
+def test_f32_edge_values_past_the_edges_never_reach_c(gpu):
+    """M = 3, N = 4, K = 36: row 0's k = 36..39 is, in memory, A[1][0..3];
+    columns 4..7 of B's row r are B[r+1][0..3].  With A[1][0] and B[5][0]
+    infinite, everything outside row 1 and column 0 must be exact."""
+    m, n, k = 3, 4, 36
+    A, B = make_inputs(m, n, k, "int", seed=36, dtype=np.float32)
+    A[1, 0] = np.inf
+    B[5, 0] = np.inf
+    C = _run(A, B, 3).astype(np.float64)
+    with np.errstate(invalid="ignore"):
+        exact = A.astype(np.float64) @ B.astype(np.float64)
+    keep = np.ones((m, n), dtype=bool)
+    keep[1, :] = False
+    keep[:, 0] = False
+    assert np.all(np.isfinite(C[keep])) and np.array_equal(C[keep], exact[keep])

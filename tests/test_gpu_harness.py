@@ -29,6 +29,7 @@ RESULT_RE = re.compile(r"TFLOPS: (?P<tf>[0-9.eE+-]+); *Average Error: (?P<err>[0
     ("task1_float16_v10", (1000, 1000, 1000), 2e-4),
     ("task1_float32_v1", (512, 384, 256), 1e-6),
     ("task1_float32_v2", (512, 512, 256), 1e-5),
+    ("task1_float32_v3", (1000, 1000, 1000), 1e-5),
 ])
 def test_task1_gpu_binary(gpu, binary, shape, bound):
     m, n, k = shape

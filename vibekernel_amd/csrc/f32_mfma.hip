@@ -83,7 +83,16 @@ __device__ __forceinline__ float4v lds_read_f4(uint32_t addr) {
   return *reinterpret_cast<const __attribute__((address_space(3))) float4v*>(addr);
 }
 
-template <int BK>
+// kEdge (version 3): the tiles may reach past M rows or N columns and the
+// last k-tile past K (any M; N, K multiples of 4).  The loads then go through
+// buffer resources over the whole matrices, the k-tile's offset in the
+// scalar offset: a lane past the end of a matrix reads zeros (A rows at or
+// below M, B k-rows at or below K); B columns past N are in range (the next
+// row's) but only feed C columns that are not stored; A's k past K on the
+// last k-tile (the next row's values, which must not meet B's zero rows: an
+// infinity would make a NaN) is masked by giving those lanes the matrix size
+// as their offset.  C elements outside M x N are not stored.
+template <int BK, bool kEdge>
 __global__ __launch_bounds__(kThreads) void f32_mfma_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                             float* __restrict__ C, int M, int N, int K) {
   using G = F32Cfg<BK>;
@@ -92,7 +101,7 @@ __global__ __launch_bounds__(kThreads) void f32_mfma_kernel(const float* __restr
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = wave >> 2, gw = wave & 3;
   int tm, tn;
-  tile_of(blockIdx.x, M / kBM, N / kBN, tm, tn);
+  tile_of(blockIdx.x, (M + (kEdge ? kBM - 1 : 0)) / kBM, (N + (kEdge ? kBN - 1 : 0)) / kBN, tm, tn);
   const int m0 = tm * kBM, n0 = tn * kBN;
   const uint32_t lds_base = lds_addr32(lds);
 
@@ -101,12 +110,14 @@ __global__ __launch_bounds__(kThreads) void f32_mfma_kernel(const float* __restr
   // number, 1 KB) ----
   constexpr int kRowsPerDma = 1024 / (4 * BK);
   uint32_t voffA[G::kDmaA], voffB[G::kDmaB];
+  uint32_t akin = 0;  // kEdge: bits 5d..5d+4 = first k of the lane's A chunk of instruction d
 #pragma unroll
   for (int d = 0; d < G::kDmaA; d++) {
     const int i = G::kDmaA * wave + d;
     const int row = kRowsPerDma * i + lane / G::kRowChunks;
     const int ca = (lane % G::kRowChunks) ^ swz_a32<BK>(row);
     voffA[d] = (uint32_t)(((size_t)row * K + ca * 4) * 4);
+    if constexpr (kEdge) akin |= (uint32_t)(ca * 4) << (5 * d);
   }
 #pragma unroll
   for (int d = 0; d < G::kDmaB; d++) {
@@ -116,14 +127,33 @@ __global__ __launch_bounds__(kThreads) void f32_mfma_kernel(const float* __restr
   }
   const char* gA = reinterpret_cast<const char*>(A) + (size_t)m0 * K * 4;
   const char* gB = reinterpret_cast<const char*>(B) + (size_t)n0 * 4;
+  const uint32_t sizeA = kEdge ? (uint32_t)M * (uint32_t)K * 4u : 0u;
+  const uint32_t sizeB = kEdge ? (uint32_t)K * (uint32_t)N * 4u : 0u;
+  const __amdgpu_buffer_rsrc_t rsrcA =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(A), 0, (int)sizeA, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rsrcB =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(B), 0, (int)sizeB, kBufferWord3);
   auto issue = [&](int kt, int slot) {
     const uint32_t s = lds_base + slot * G::kStageBytes;
+    if constexpr (kEdge) {
+      const uint32_t kleft = (uint32_t)(K - kt * BK);  // k from this k-tile's start to K (> 0)
+      const uint32_t soffA = (uint32_t)(m0 * K + kt * BK) * 4u;
+      const uint32_t soffB = (uint32_t)(kt * BK * N + n0) * 4u;
 #pragma unroll
-    for (int d = 0; d < G::kDmaA; d++)
-      dma16(gA + (size_t)kt * BK * 4, voffA[d], s + (G::kDmaA * wave + d) * 1024);
+      for (int d = 0; d < G::kDmaA; d++) {
+        const uint32_t off = ((akin >> (5 * d)) & 31u) < kleft ? voffA[d] : sizeA;  // sizeA: zeros
+        dma16_buf(rsrcA, off, soffA, s + (G::kDmaA * wave + d) * 1024);
+      }
 #pragma unroll
-    for (int d = 0; d < G::kDmaB; d++)
-      dma16(gB + (size_t)kt * BK * N * 4, voffB[d], s + G::kABytes + (G::kDmaB * wave + d) * 1024);
+      for (int d = 0; d < G::kDmaB; d++) dma16_buf(rsrcB, voffB[d], soffB, s + G::kABytes + (G::kDmaB * wave + d) * 1024);
+    } else {
+#pragma unroll
+      for (int d = 0; d < G::kDmaA; d++)
+        dma16(gA + (size_t)kt * BK * 4, voffA[d], s + (G::kDmaA * wave + d) * 1024);
+#pragma unroll
+      for (int d = 0; d < G::kDmaB; d++)
+        dma16(gB + (size_t)kt * BK * N * 4, voffB[d], s + G::kABytes + (G::kDmaB * wave + d) * 1024);
+    }
   };
 
   // ---- fragment addresses inside a stage: lane half h takes k = (BK/2) h
@@ -155,7 +185,7 @@ __global__ __launch_bounds__(kThreads) void f32_mfma_kernel(const float* __restr
       for (int r = 0; r < 16; r++) acc[bi][bj][r] = 0.0f;
   prefer_agpr_accumulators();
 
-  const int nk = K / BK;
+  const int nk = (K + (kEdge ? BK - 1 : 0)) / BK;
 #pragma unroll
   for (int st = 0; st < G::kNS - 1; st++) issue(min(st, nk - 1), st);
 
@@ -192,27 +222,28 @@ __global__ __launch_bounds__(kThreads) void f32_mfma_kernel(const float* __restr
   // ---- epilogue: lane l, register r of block (bi, bj) ->
   // row 8*(r/4) + 4*(l/32) + r%4, column l%32: 128-byte row segments ----
   const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
-  float* Cw = C + (size_t)(m0 + grp * 128) * N + n0 + gw * 64;
+  const int row0 = m0 + grp * 128, col0 = n0 + gw * 64;
 #pragma unroll
   for (int bi = 0; bi < 4; bi++)
 #pragma unroll
     for (int bj = 0; bj < 2; bj++)
 #pragma unroll
       for (int r = 0; r < 16; r++) {
-        const int row = bi * 32 + 8 * (r >> 2) + 4 * (lane_e >> 5) + (r & 3);
-        Cw[(size_t)row * N + bj * 32 + (lane_e & 31)] = acc[bi][bj][r];
+        const int row = row0 + bi * 32 + 8 * (r >> 2) + 4 * (lane_e >> 5) + (r & 3);
+        const int col = col0 + bj * 32 + (lane_e & 31);
+        if (!kEdge || (row < M && col < N)) C[(size_t)row * N + col] = acc[bi][bj][r];
       }
 }
 
 // 32-deep k-tiles when K allows (one barrier per 128 MFMAs of a wave:
 // measured 141.2 against 139.6 TFLOP/s at 4096^3), else 16-deep.
-template <int BK>
+template <int BK, bool kEdge = false>
 hipError_t launch_bk(const GemmArgs& a) {
   static std::atomic<uint64_t> attr_done{0};
-  auto kfn = f32_mfma_kernel<BK>;
+  auto kfn = f32_mfma_kernel<BK, kEdge>;
   hipError_t e = ensure_lds_attr(kfn, F32Cfg<BK>::kLdsBytes, a.device, attr_done);
   if (e != hipSuccess) return e;
-  const int tiles = (int)((a.m / kBM) * (a.n / kBN));
+  const int tiles = kEdge ? (int)(((a.m + kBM - 1) / kBM) * ((a.n + kBN - 1) / kBN)) : (int)((a.m / kBM) * (a.n / kBN));
   hipLaunchKernelGGL(kfn, dim3(tiles), dim3(kThreads), F32Cfg<BK>::kLdsBytes, a.stream,
                      static_cast<const float*>(a.A), static_cast<const float*>(a.B), static_cast<float*>(a.C),
                      (int)a.m, (int)a.n, (int)a.k);
@@ -229,6 +260,15 @@ bool f32_mfma_shape_ok(size_t m, size_t n, size_t k) {
          (m / kBM) * (n / kBN) < (1ull << 31);
 }
 
+// Version 3 (any M; N, K multiples of 4): 32-deep k-tiles, the last one
+// masked; each operand below 2^31 bytes (buffer sizes and offsets).
+hipError_t launch_f32_mfma_edge(const GemmArgs& a) { return launch_bk<32, true>(a); }
+
+bool f32_mfma_edge_shape_ok(size_t m, size_t n, size_t k) {
+  return m >= 1 && n >= 4 && k >= 4 && m * k * 4 < (1ull << 31) && k * n * 4 < (1ull << 31) &&
+         f32_mfma_shape_ok(((m + kBM - 1) / kBM) * kBM, ((n + kBN - 1) / kBN) * kBN, k);
+}
+
 }  // namespace
 
 void register_f32_mfma() {
@@ -241,6 +281,14 @@ void register_f32_mfma() {
   e.workspace = nullptr;
   e.shape_ok = f32_mfma_shape_ok;
   register_kernel(e);
+
+  KernelEntry e3 = e;
+  e3.version = 3;
+  e3.name = "f32_v3_mfma256_edge";
+  e3.caps = make_caps(3, VK_DTYPE_F32, kOutF32, 1, 4, 4, 16, kBM, kBN, 32, kThreads, F32Cfg<32>::kLdsBytes, 0, 0);
+  e3.launch = launch_f32_mfma_edge;
+  e3.shape_ok = f32_mfma_edge_shape_ok;
+  register_kernel(e3);
 }
 
 }  // namespace vk

@@ -106,7 +106,7 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
     convenience of the front end."""
     in_dt = DTYPE_F16 if dtype == "f16" else DTYPE_F32
     out_dt = DTYPE_F16 if (out or dtype) == "f16" else DTYPE_F32
-    order = [8, 4, 9, 7, 10, 6, 5, 3, 2, 1] if in_dt == DTYPE_F16 else [2, 1]
+    order = [8, 4, 9, 7, 10, 6, 5, 3, 2, 1] if in_dt == DTYPE_F16 else [2, 3, 1]
     avail = set(_abi.versions(in_dt))
     for v in order:
         if v == 9 and _abi.workspace_bytes(v, in_dt, m, n, k) == 0:
