@@ -136,7 +136,10 @@ def test_pick_version_follows_shape():
     assert vk.pick_version(16, 8192, 8192) == 8
     assert vk.pick_version(16, 8224, 8192) == 4  # n % 128 != 0: the 32-column kernel
     assert vk.pick_version(128, 8192, 8192) == 8  # batch-128 decode: still the split-K kernel
-    assert vk.pick_version(144, 8192, 8192) == 10  # beyond 128 rows: v7 with edges
+    assert vk.pick_version(144, 8192, 8192) == 8  # 2 x 2 waves up to 256 rows
+    assert vk.pick_version(1, 8192, 8192) == 8    # one row: the same kernel, rows past M read as zeros
+    assert vk.pick_version(256, 8192, 8192) == 8
+    assert vk.pick_version(300, 8192, 8192) == 10  # beyond 256 rows: v7 with edges
     assert vk.pick_version(4096, 4096, 4096) == 7  # 256 tiles: one full wave
     assert vk.pick_version(4096, 4096, 4096, "f16", "f32") == 7
     assert vk.pick_version(4096, 11008, 4096) == 7  # 688 tiles = 2.69 waves: tail left whole

@@ -20,7 +20,9 @@ TILE_SHAPES = [(256, 256, 64), (512, 256, 128), (256, 512, 192), (768, 512, 256)
 ANY_SHAPES = [(1, 1, 1), (17, 33, 65), (127, 129, 31), (200, 300, 100), (256, 256, 64), (64, 8, 1000)]
 EDGE_SHAPES = [(1, 8, 8), (17, 40, 72), (100, 264, 136), (255, 256, 64), (257, 520, 200), (300, 1000, 520)]
 SKINNY_SHAPES = [(16, 256, 512), (32, 512, 1024), (48, 96, 128), (64, 128, 256), (16, 2048, 4096),
-                 (80, 256, 512), (96, 384, 96), (112, 128, 1024), (128, 1024, 2048)]
+                 (80, 256, 512), (96, 384, 96), (112, 128, 1024), (128, 1024, 2048),
+                 (1, 128, 32), (5, 256, 512), (17, 384, 1024), (144, 256, 512), (170, 512, 1024),
+                 (176, 128, 96), (161, 1024, 2048), (200, 512, 1024), (250, 128, 96), (256, 1024, 2048)]
 
 
 def _versions():
@@ -36,7 +38,7 @@ def _shapes_for(version):
         shapes = ANY_SHAPES + shapes[:2]
     elif c.div_m == 1:
         shapes = EDGE_SHAPES + shapes[:2]
-    if c.max_m <= 128:
+    if c.max_m <= 256:
         shapes = [s for s in SKINNY_SHAPES if s[0] <= c.max_m and s[0] % c.div_m == 0
                   and s[1] % c.div_n == 0 and s[2] % c.div_k == 0]
     return shapes
@@ -238,10 +240,11 @@ def test_mlp_shapes(gpu, oracle, shape, version):
 
 
 @pytest.mark.slow
-@pytest.mark.parametrize("version,m", [(4, 16), (8, 16), (8, 128)])
+@pytest.mark.parametrize("version,m", [(4, 16), (8, 16), (8, 128), (8, 1), (8, 200)])
 def test_skinny_decode_shape(gpu, oracle, version, m):
-    """M = 16 or 128, N = K = 8192 (the decode-like, HBM-bound configurations)
-    on the skinny kernels, fp16 and fp32 output, against the oracle."""
+    """M = 1, 16, 128 or 200, N = K = 8192 (the decode-like, HBM-bound
+    configurations) on the skinny kernels, fp16 and fp32 output, against the
+    oracle."""
     n, k = 8192, 8192
     A, B = make_inputs(m, n, k, "uniform", seed=16)
     C64 = oracle.dgemm(A, B)
@@ -286,7 +289,7 @@ def test_splitk_skinny_shape_sequence(gpu, oracle):
     partials must leave the next call's counters zero (they once overlapped
     the counters of a wider call), so every call matches the oracle."""
     shapes = [(16, 128, 4096), (128, 256, 2048), (16, 8192, 8192), (32, 28672, 1024), (16, 16384, 1024),
-              (48, 384, 2048), (128, 8192, 1024), (16, 128, 4096)]
+              (48, 384, 2048), (128, 8192, 1024), (200, 1024, 2048), (1, 8192, 1024), (256, 512, 4096), (16, 128, 4096)]
     for m, n, k in shapes:
         A, B = make_inputs(m, n, k, "uniform", seed=m + n + k)
         C = run_gemm(8, A, B, "f32")
@@ -320,7 +323,7 @@ def test_splitk_skinny_caller_workspace(gpu, oracle):
     assert small == -6  # VK_ERR_WORKSPACE
 
 
-@pytest.mark.parametrize("version,m", [(4, 80), (8, 144)])
+@pytest.mark.parametrize("version,m", [(4, 80), (8, 272)])
 def test_skinny_rejects_wide_m(gpu, version, m):
     import torch
     import vibekernel_amd as vk

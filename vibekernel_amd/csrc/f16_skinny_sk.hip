@@ -1,4 +1,4 @@
-// f16_skinny_sk.hip -- fp16 GEMM for skinny A (decode-like: M <= 128), version 8:
+// f16_skinny_sk.hip -- fp16 GEMM for skinny A (decode-like: any M <= 256), version 8:
 // split-K over workgroups with a deterministic in-kernel reduction.
 //
 // Same job as version 4 (f16_skinny.hip); the reference has no path for this
@@ -54,8 +54,16 @@ constexpr int kWaves = 4;
 constexpr int kThreads = kWaves * 64;
 constexpr int kKStep = 32;     // k per stage (one 16x16x32 MFMA deep)
 
-template <int NC, int MB>  // NC columns per workgroup, M <= 16 * MB rows
+// NC columns per workgroup, M <= 16 * MB rows.  Up to 8 row blocks every
+// wave holds all rows and NC/4 columns; beyond (MB even) the waves form 2 x 2,
+// each holding half the rows and NC/2 columns, which halves the A fragments a
+// wave reads per k-step.
+template <int NC, int MB>
 struct SkCfg {
+  static constexpr int kWR = MB > 8 ? 2 : 1;                    // wave rows
+  static constexpr int kWC = kWaves / kWR;                      // wave columns
+  static constexpr int kMBW = MB / kWR;                         // row blocks per wave
+  static_assert(MB % kWR == 0 && MB <= 4 * kWaves, "row blocks");
   static constexpr int kChunks = NC / 8;                        // 16-byte chunks per B row
   static constexpr int kRowsPerDma = 1024 / (NC * 2);           // B rows per 1 KB load
   static constexpr int kBDma = 8 / kRowsPerDma;                 // B loads per wave per k-step
@@ -64,11 +72,10 @@ struct SkCfg {
   static constexpr int kStageBytes = kBStageBytes + kAStageBytes;
   static constexpr int kStages = (159 * 1024) / kStageBytes < 8 ? (159 * 1024) / kStageBytes : 8;
   static constexpr int kLdsBytes = kStages * kStageBytes;
-  static constexpr int kWaveCols = NC / kWaves;                 // 32 or 64
+  static constexpr int kWaveCols = NC / kWC;                   // 32, 64 or 128
   static constexpr int kColBlocks = kWaveCols / 16;             // per wave
   static_assert(kStages >= 4, "pipeline depth");
-  static constexpr int kMaxADma = MB > kWaves ? 2 : 1;         // A loads per wave per k-step
-  static_assert(MB <= 2 * kWaves, "A blocks per k-step");
+  static constexpr int kMaxADma = (MB + kWaves - 1) / kWaves;  // A loads per wave per k-step
   static_assert((kStages - 1) * (kBDma + kMaxADma) <= 63, "vmcnt range");
 };
 
@@ -131,9 +138,10 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
 
   // Direct-to-LDS duty per k-step.  B: load i covers k-rows 8w + i*R .. +R-1
   // (R = 1024 / (2 NC) rows of NC/8 chunks; lane l: row l / (NC/8), slot
-  // l % (NC/8)).  A: wave w covers rows 16w .. 16w+15 if w < MB and rows
-  // 16(w+4) .. +15 if w + 4 < MB (4 chunks each; lane l: row l/4, slot l%4;
-  // the swizzle of row r + 64 is that of row r).
+  // l % (NC/8)).  A: wave w covers the 16-row blocks w + 4j < MB (4 chunks
+  // per row; lane l: row l/4, slot l%4; the swizzle of row r + 64 is that of
+  // row r); a row past M loads row M - 1 instead (valid memory; the rows
+  // past M are never stored).
   uint32_t offB[G::kBDma];
 #pragma unroll
   for (int i = 0; i < G::kBDma; i++) {
@@ -142,22 +150,33 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
     offB[i] = (uint32_t)(((size_t)krow * N + c * 8) * 2);
   }
   const int arow = 16 * wave + (lane >> 2);
-  const uint32_t offA = (uint32_t)(((size_t)arow * K + (((lane & 3) ^ swz_a64(arow)) * 8)) * 2);
+  uint32_t offA[G::kMaxADma];
+#pragma unroll
+  for (int j = 0; j < G::kMaxADma; j++) {
+    const int row = min(arow + 64 * j, M - 1);
+    offA[j] = (uint32_t)(((size_t)row * K + (((lane & 3) ^ swz_a64(arow)) * 8)) * 2);
+  }
   const char* gB = reinterpret_cast<const char*>(B) + ((size_t)kbeg * N + n0) * 2;
   const char* gA = reinterpret_cast<const char*>(A) + (size_t)kbeg * 2;
-  const char* gA4 = gA + (size_t)64 * K * 2;  // rows 64 .. 127
   const uint32_t lbase = lds_addr32(lds);
-  const int na = (wave < MB) + (wave + kWaves < MB);  // A loads of this wave per k-step (wave-uniform)
+  int na = 0;  // A loads of this wave per k-step (wave-uniform)
+#pragma unroll
+  for (int j = 0; j < G::kMaxADma; j++) na += wave + kWaves * j < MB;
 
-  auto issue = [&](int stage, int step) {
+  // NA = this wave's A loads per k-step (blocks wave + 4j < MB are j < NA).
+  auto issue = [&](auto nac, int stage, int step) {
+    constexpr int NA = decltype(nac)::value;
     const uint32_t s = lbase + stage * G::kStageBytes;
     const size_t kb = (size_t)step * kKStep;
 #pragma unroll
     for (int i = 0; i < G::kBDma; i++) dma16(gB + kb * N * 2, offB[i], s + (8 * wave + i * G::kRowsPerDma) * NC * 2);
-    if (wave < MB) dma16(gA + kb * 2, offA, s + G::kBStageBytes + wave * 1024);
-    if (G::kMaxADma == 2 && wave + kWaves < MB)
-      dma16(gA4 + kb * 2, offA, s + G::kBStageBytes + (wave + kWaves) * 1024);
+#pragma unroll
+    for (int j = 0; j < NA; j++) dma16(gA + kb * 2, offA[j], s + G::kBStageBytes + (wave + kWaves * j) * 1024);
   };
+  // This wave's row and column group (compile-time 0 and `wave` when the
+  // waves do not split the rows, so the fragment offsets stay immediates).
+  const int rg = G::kWR == 1 ? 0 : wave / G::kWC;
+  const int cg = G::kWR == 1 ? wave : wave % G::kWC;
 
   // Fragment addresses inside a stage.
   // B (MFMA B operand, 16x16x32): lane 16g + 4jj + q names k-row
@@ -168,24 +187,26 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
   uint32_t boff[G::kColBlocks];
 #pragma unroll
   for (int c = 0; c < G::kColBlocks; c++) {
-    const int chunk = (G::kWaveCols / 8) * wave + 2 * c + (q >> 1);
+    const int chunk = (G::kWaveCols / 8) * cg + 2 * c + (q >> 1);
     boff[c] = (uint32_t)(krow0 * NC * 2 + 16 * (chunk ^ swz_bk<NC>(krow0)) + 8 * (q & 1));
   }
   // A (MFMA A operand): lane l holds A[l%16][8*(l/16) .. +7]: row l%16,
   // chunk l/16 of that row.
   const int ar = lane & 15;
-  const uint32_t aoff = (uint32_t)(G::kBStageBytes + ar * 64 + 16 * ((lane >> 4) ^ swz_a64(ar)));
+  const uint32_t aoff = (uint32_t)(G::kBStageBytes + ar * 64 + 16 * ((lane >> 4) ^ swz_a64(ar))) +
+                        (uint32_t)(rg * G::kMBW * 1024);  // this wave's first row block
 
-  float4v acc[MB][G::kColBlocks];
+  constexpr int MBW = G::kMBW;
+  float4v acc[MBW][G::kColBlocks];
 #pragma unroll
-  for (int r = 0; r < MB; r++)
+  for (int r = 0; r < MBW; r++)
 #pragma unroll
     for (int c = 0; c < G::kColBlocks; c++) acc[r][c] = float4v{0.f, 0.f, 0.f, 0.f};
 
-  // Fragments of one k-step: B for this wave's column blocks, A for all rows.
+  // Fragments of one k-step: B for this wave's column blocks, A for its rows.
   struct Frags {
     half8 b[G::kColBlocks];
-    half8 a[MB];
+    half8 a[MBW];
   };
   auto read_frags = [&](Frags& f, int stage) {
     const uint32_t sb = lbase + stage * G::kStageBytes;
@@ -196,63 +217,68 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
       f.b[c] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
     }
 #pragma unroll
-    for (int r = 0; r < MB; r++) f.a[r] = lds_read_h8(sb + aoff + r * 1024);
+    for (int r = 0; r < MBW; r++) f.a[r] = lds_read_h8(sb + aoff + r * 1024);
   };
-  // This wave's loads of a step have landed when at most `ahead` later steps
-  // of its loads are still in flight.
-  auto wait_steps = [&](auto ahead) {
-    constexpr int H = decltype(ahead)::value;
-    if (G::kMaxADma == 2 && na == 2)
-      wait_vmcnt<H * (G::kBDma + G::kMaxADma)>();
-    else if (na >= 1)
-      wait_vmcnt<H * (G::kBDma + 1)>();
-    else
-      wait_vmcnt<H * G::kBDma>();
-  };
-
   // Software pipeline over a ring of S stages: iteration `step` multiplies
   // the fragments of `step` (read during the previous iteration) while the
   // fragments of step + 1 are read, so the LDS reads of one k-step overlap
   // the MFMAs of the one before; the stage of `step` is refilled with step
   // + S once every wave's reads of it are done (barrier).  Clamped refills
-  // of a short k range land in stages whose contents are never used.
+  // of a short k range land in stages whose contents are never used.  The
+  // loop is instantiated per count of A loads (NA, fixed for a wave), so a
+  // k-step waits with a constant count and issues without branches (a
+  // cascade of tests on the count cost ~2 us per launch at M = 128).
+  auto pipeline = [&](auto nac) {
+    constexpr int LOADS = G::kBDma + decltype(nac)::value;  // this wave's loads per k-step
 #pragma unroll
-  for (int st = 0; st < S; st++) issue(st, min(st, nsteps - 1));
-  Frags f[2];
-  wait_steps(std::integral_constant<int, S - 1>{});
-  lds_barrier();
-  read_frags(f[0], 0);
-  auto iteration = [&](int step, Frags& cur, Frags& next) {
-    // This wave's loads of step + 1 landed, then everyone's (barrier); the
-    // barrier also ends every wave's reads of `step`'s stage.
-    wait_steps(std::integral_constant<int, S - 2>{});
-    wait_lgkmcnt0();  // as the barrier's own wait, but visible to the compiler:
-                      // it then knows `cur` has landed and waits for no read
-                      // of `next` before the MFMAs
+    for (int st = 0; st < S; st++) issue(nac, st, min(st, nsteps - 1));
+    Frags f[2];
+    wait_vmcnt<(S - 1) * LOADS>();
     lds_barrier();
-    issue(step % S, min(step + S, nsteps - 1));
-    read_frags(next, (step + 1) % S);
-    __builtin_amdgcn_sched_barrier(0);
+    read_frags(f[0], 0);
+    auto iteration = [&](int step, Frags& cur, Frags& next) {
+      // This wave's loads of step + 1 landed, then everyone's (barrier); the
+      // barrier also ends every wave's reads of `step`'s stage.
+      wait_vmcnt<(S - 2) * LOADS>();
+      wait_lgkmcnt0();  // as the barrier's own wait, but visible to the compiler:
+                        // it then knows `cur` has landed and waits for no read
+                        // of `next` before the MFMAs
+      lds_barrier();
+      issue(nac, step % S, min(step + S, nsteps - 1));
+      read_frags(next, (step + 1) % S);
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-    for (int r = 0; r < MB; r++)
+      for (int r = 0; r < MBW; r++)
 #pragma unroll
-      for (int c = 0; c < G::kColBlocks; c++) acc[r][c] = mfma16x16x32(cur.a[r], cur.b[c], acc[r][c]);
+        for (int c = 0; c < G::kColBlocks; c++) acc[r][c] = mfma16x16x32(cur.a[r], cur.b[c], acc[r][c]);
+    };
+    for (int step = 0; step < nsteps; step += 2) {
+      iteration(step, f[0], f[1]);
+      if (step + 1 < nsteps) iteration(step + 1, f[1], f[0]);
+    }
   };
-  for (int step = 0; step < nsteps; step += 2) {
-    iteration(step, f[0], f[1]);
-    if (step + 1 < nsteps) iteration(step + 1, f[1], f[0]);
-  }
+  // A wave loads MB / 4 or MB / 4 + 1 blocks (0 or 1 below 4).
+  constexpr int kNaHi = G::kMaxADma, kNaLo = MB / kWaves;
+  if constexpr (kNaHi == kNaLo)
+    pipeline(std::integral_constant<int, kNaHi>{});
+  else if (na == kNaHi)
+    pipeline(std::integral_constant<int, kNaHi>{});
+  else
+    pipeline(std::integral_constant<int, kNaLo>{});
   wait_vmcnt<0>();  // clamped tail refills
 
   // Epilogue.  D layout: lane l, register e of block (r, c) -> row
   // 16 r + 4 (l / 16) + e, column kWaveCols * w + 16 c + l % 16 of the block.
-  constexpr int NB = MB * G::kColBlocks;  // 16 x 16 blocks per wave
-  OutT* Cw = C + n0 + G::kWaveCols * wave + (lane & 15);
-  const int rq = 4 * (lane >> 4);
+  constexpr int NB = MBW * G::kColBlocks;  // 16 x 16 blocks per wave
+  OutT* Cw = C + n0 + G::kWaveCols * cg + (lane & 15);
+  const int rq = 16 * rg * MBW + 4 * (lane >> 4);
   auto store_c = [&](int b, const float4v& v) {
     const int r = b / G::kColBlocks, c = b % G::kColBlocks;
 #pragma unroll
-    for (int e = 0; e < 4; e++) Cw[(size_t)(16 * r + rq + e) * N + 16 * c] = convert_out<OutT>(v[e]);
+    for (int e = 0; e < 4; e++) {
+      const int row = 16 * r + rq + e;
+      if (row < M) Cw[(size_t)row * N + 16 * c] = convert_out<OutT>(v[e]);
+    }
   };
   if (ks_count == 1) {
 #pragma unroll
@@ -331,11 +357,18 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
 // the same place for every shape, which keeps the library workspace clean
 // (all counters zero) from one call to the next whatever the shapes.
 // Unsplit shapes need no workspace.
+// Row blocks of the instance that serves M rows (even beyond 8: 2 x 2 waves).
+constexpr int kMaxRows = 256;
+
+int pick_mb(size_t m) {
+  const int mb = (int)((m + 15) / 16);
+  return mb > 8 ? (mb + 1) & ~1 : mb;
+}
+
 size_t sk_workspace(size_t m, size_t n, size_t k, int num_cus) {
   const int ks = pick_ks(n, k, num_cus);
   if (ks == 1) return 0;
-  const size_t mb = (m + 15) / 16;
-  return kCounterBytes + (size_t)ks * n * 16 * mb * sizeof(float);
+  return kCounterBytes + (size_t)ks * n * 16 * pick_mb(m) * sizeof(float);
 }
 
 template <int NC, int MB, typename OutT>
@@ -371,7 +404,7 @@ hipError_t launch_mb(const GemmArgs& a) {
 
 template <int NC>
 hipError_t launch_nc(const GemmArgs& a) {
-  switch ((a.m + 15) / 16) {
+  switch (pick_mb(a.m)) {
     case 1: return launch_mb<NC, 1>(a);
     case 2: return launch_mb<NC, 2>(a);
     case 3: return launch_mb<NC, 3>(a);
@@ -379,17 +412,23 @@ hipError_t launch_nc(const GemmArgs& a) {
     case 5: return launch_mb<NC, 5>(a);
     case 6: return launch_mb<NC, 6>(a);
     case 7: return launch_mb<NC, 7>(a);
-    default: return launch_mb<NC, 8>(a);
+    case 8: return launch_mb<NC, 8>(a);
+    case 10: return launch_mb<NC, 10>(a);
+    case 12: return launch_mb<NC, 12>(a);
+    case 14: return launch_mb<NC, 14>(a);
+    default: return launch_mb<NC, 16>(a);
   }
 }
 
 hipError_t launch_sk(const GemmArgs& a) { return launch_nc<128>(a); }
 
-// M a multiple of 16 up to 128; N a multiple of 128; K a multiple of 32; the
-// per-lane 32-bit byte offsets (up to 64 rows of A from either base, 32 rows
-// of B) must not overflow.
+// Any M up to 256 (measured at N = K = 8192, µs per launch, this kernel
+// against the 256-row tiles of versions 10 / 9: M = 200 49.1 / 54.6, 224
+// 48.6 / 55.0, 256 53.2 / 54.7); N a multiple of 128; K a multiple of 32; the
+// 32-bit lane byte offsets into A (up to 256 rows) and B (32 rows) must not
+// overflow.
 bool sk_shape_ok(size_t m, size_t n, size_t k) {
-  return m >= 16 && m <= 128 && (size_t)64 * k * 2 < (1ull << 31) && (size_t)32 * n * 2 < (1ull << 31) &&
+  return m >= 1 && m <= kMaxRows && (size_t)256 * k * 2 < (1ull << 31) && (size_t)32 * n * 2 < (1ull << 31) &&
          (n / 128) * 8 < (1ull << 31);
 }
 
@@ -400,8 +439,8 @@ void register_f16_skinny_sk() {
   e.version = 8;
   e.in_dtype = VK_DTYPE_F16;
   e.name = "f16_v8_skinny_splitk";
-  e.caps = make_caps(8, VK_DTYPE_F16, kOutF16 | kOutF32, 16, 128, kKStep, 16, 128, 128, kKStep, kThreads,
-                     SkCfg<128, 8>::kLdsBytes, 0, 1, 128);
+  e.caps = make_caps(8, VK_DTYPE_F16, kOutF16 | kOutF32, 1, 128, kKStep, 16, 256, 128, kKStep, kThreads,
+                     SkCfg<128, 16>::kLdsBytes, 0, 1, kMaxRows);
   e.launch = launch_sk;
   e.workspace = sk_workspace;
   e.shape_ok = sk_shape_ok;
