@@ -96,7 +96,7 @@ def query(version: int, dtype: str = "f16"):
 def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = None) -> int:
     """The fastest version that accepts this shape (checked with vk_gemm_check
     on 4 KiB-aligned placeholder addresses; nothing is launched): for fp16
-    the skinny kernels when M <= 128 (64 for version 4), then the 256x256
+    the skinny kernels when M <= 256 (64 for version 4), then the 256x256
     kernels (fastest first; version 10 takes shapes off the 256 x 256 x 64
     grid whose N and K are multiples of 8), then the any-shape kernel.  The
     split-tail version 9 comes first among the 256x256 kernels only where its
