@@ -1,7 +1,8 @@
 """ctypes front end of the CPU oracle (oracle/vk_oracle.c).
 
 TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()``
-as the checker, and by bench.py's cpu_baseline leg as the timed CPU baseline.
+to verify its result, and by bench.py's cpu_baseline leg as the timed CPU
+baseline.
 The product never imports it.
 
 Every function follows a reference file (paths relative to the reference
