@@ -1,0 +1,50 @@
+"""End to end through the version pick: for shapes that land on each fp16
+and fp32 version, pick_version's choice runs on the GPU and its result is
+checked against the exact (fp64) product with the fp32 accumulation bound
+(tests/gpu_util.py)."""
+import numpy as np
+import pytest
+
+from gpu_util import check_f32_out, make_inputs, run_gemm
+
+pytestmark = pytest.mark.gpu
+
+F16_CASES = [
+    ((1, 256, 64), 8),           # one row: the skinny split-K kernel
+    ((200, 1024, 2048), 8),      # 2 x 2 waves
+    ((16, 8224, 256), 4),        # n % 128 != 0: the 32-column skinny kernel
+    ((512, 512, 512), 7),        # on the 256 x 256 x 64 grid
+    ((2048, 2048, 4096), 9),     # 64 tiles: split tail
+    ((300, 264, 72), 10),        # off the grid
+    ((1000, 1000, 4000), 10),    # off the grid, split tail
+    ((512, 512, 544), 10),       # k % 64 != 0
+    ((100, 300, 70), 1),         # n % 8 != 0: any shape
+]
+F32_CASES = [
+    ((512, 512, 512), 2),
+    ((500, 512, 512), 3),
+    ((500, 510, 512), 1),
+]
+
+
+@pytest.mark.parametrize("shape,expected", F16_CASES)
+def test_f16_pick_runs_and_matches(gpu, oracle, shape, expected):
+    import vibekernel_amd as vk
+    m, n, k = shape
+    v = vk.pick_version(m, n, k)
+    assert v == expected
+    A, B = make_inputs(m, n, k, "uniform", seed=m + 3 * n + 7 * k)
+    check_f32_out(run_gemm(v, A, B, "f32"), A, B, oracle.dgemm(A, B))
+
+
+@pytest.mark.parametrize("shape,expected", F32_CASES)
+def test_f32_pick_runs_and_matches(gpu, oracle, shape, expected):
+    import vibekernel_amd as vk
+    m, n, k = shape
+    v = vk.pick_version(m, n, k, "f32")
+    assert v == expected
+    A, B = make_inputs(m, n, k, "uniform", seed=m + n + k, dtype=np.float32)
+    C = run_gemm(v, A, B, "f32")
+    C64 = oracle.dgemm(A, B)
+    bound = 2.0 * k * 2.0 ** -24 * (np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64))
+    assert np.all(np.abs(C - C64) <= bound + 1e-30)
