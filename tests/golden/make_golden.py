@@ -29,6 +29,9 @@ CASES = [
     ("f16_16x256x512_uniform", np.float16, (16, 256, 512), "uniform", 16256),
     ("f32_64x96x128_uniform", np.float32, (64, 96, 128), "uniform", 6496),
     ("f32_256x256x32_int", np.float32, (256, 256, 32), "int", 25632),
+    ("f16_300x264x72_int", np.float16, (300, 264, 72), "int", 30026),
+    ("f16_1x256x96_uniform", np.float16, (1, 256, 96), "uniform", 1256),
+    ("f32_100x260x36_uniform", np.float32, (100, 260, 36), "uniform", 10026),
 ]
 
 
@@ -57,6 +60,8 @@ def make(name, dtype, shape, dist, seed):
 
 
 if __name__ == "__main__":
+    # make_golden.py [name ...]: only the named fixtures (all when none)
     for case in CASES:
-        make(*case)
-        print("wrote", case[0])
+        if len(sys.argv) == 1 or case[0] in sys.argv[1:]:
+            make(*case)
+            print("wrote", case[0])
