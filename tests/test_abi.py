@@ -134,7 +134,8 @@ def test_single_hip_runtime_in_process():
 def test_pick_version_follows_shape():
     import vibekernel_amd as vk
     assert vk.pick_version(16, 8192, 8192) == 8
-    assert vk.pick_version(16, 8224, 8192) == 4  # n % 128 != 0: the 32-column kernel
+    assert vk.pick_version(16, 8224, 8192) == 8  # n % 128 != 0: the last column block cut short
+    assert vk.pick_version(16, 8220, 8192) == 1  # n % 8 != 0: the any-shape kernel
     assert vk.pick_version(128, 8192, 8192) == 8  # batch-128 decode: still the split-K kernel
     assert vk.pick_version(144, 8192, 8192) == 8  # 2 x 2 waves up to 256 rows
     assert vk.pick_version(1, 8192, 8192) == 8    # one row: the same kernel, rows past M read as zeros

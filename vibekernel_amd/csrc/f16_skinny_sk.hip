@@ -10,7 +10,7 @@
 // strip 6.4 TB/s, 256-byte strips with K split over 4 workgroups 6.7 TB/s.
 // Version 4 owns 64-byte strips.  Here:
 //  * a workgroup owns NC = 128 columns (256-byte rows of B; the kernel is
-//    written for NC = 256 as well) and 1/KS of K; grid = (N / NC) x KS with
+//    written for NC = 256 as well) and 1/KS of K; grid = ceil(N / NC) x KS with
 //    KS the largest power of two (up to 8) that keeps the grid within one
 //    workgroup per CU (KS = 4 at N = 8192 on 256 CUs);
 //  * 4 waves; per 32-deep k-step each wave loads 8 rows of B (direct-to-LDS,
@@ -110,7 +110,7 @@ constexpr size_t kCounterBytes = 4096;
 // 23 / 21 / 25 / 36; 128 x 8192 x 8192 (64): 86 / 49 / 33 / 54 -- a second
 // round of workgroups costs more than the longer k range of each.
 int pick_ks(size_t n, size_t k, int num_cus) {
-  const size_t ncb = n / pick_nc(n);
+  const size_t ncb = (n + pick_nc(n) - 1) / pick_nc(n);
   int ks = 1;
   while (ks < 8 && ncb * ks * 2 <= (size_t)num_cus && k % ((size_t)kKStep * ks * 2) == 0 &&
          ncb * kWaves * sizeof(unsigned) <= kCounterBytes)
@@ -143,11 +143,15 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
   // per row; lane l: row l/4, slot l%4; the swizzle of row r + 64 is that of
   // row r); a row past M loads row M - 1 instead (valid memory; the rows
   // past M are never stored).
+  // In a last column block that N cuts short (N a multiple of 8), a lane
+  // whose chunk lies past N loads the block's last chunk of the same row
+  // instead: valid memory, and the columns past N are never stored.
+  const int cvalid = min(NC, N - n0) / 8;
   uint32_t offB[G::kBDma];
 #pragma unroll
   for (int i = 0; i < G::kBDma; i++) {
     const int krow = 8 * wave + i * G::kRowsPerDma + lane / G::kChunks;
-    const int c = (lane % G::kChunks) ^ swz_bk<NC>(krow);
+    const int c = min((lane % G::kChunks) ^ swz_bk<NC>(krow), cvalid - 1);
     offB[i] = (uint32_t)(((size_t)krow * N + c * 8) * 2);
   }
   const int arow = 16 * wave + (lane >> 2);
@@ -271,10 +275,12 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
   // Epilogue.  D layout: lane l, register e of block (r, c) -> row
   // 16 r + 4 (l / 16) + e, column kWaveCols * w + 16 c + l % 16 of the block.
   constexpr int NB = MBW * G::kColBlocks;  // 16 x 16 blocks per wave
-  OutT* Cw = C + n0 + G::kWaveCols * cg + (lane & 15);
+  const int col0 = n0 + G::kWaveCols * cg + (lane & 15);
+  OutT* Cw = C + col0;
   const int rq = 16 * rg * MBW + 4 * (lane >> 4);
   auto store_c = [&](int b, const float4v& v) {
     const int r = b / G::kColBlocks, c = b % G::kColBlocks;
+    if (col0 + 16 * c >= N) return;  // past N (a last column block cut short)
 #pragma unroll
     for (int e = 0; e < 4; e++) {
       const int row = 16 * r + rq + e;
@@ -299,7 +305,7 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
   constexpr uint32_t kWaveRegion = NB * 1024;
   constexpr uint32_t kSlotBytes = kWaves * kWaveRegion;
   const __amdgpu_buffer_rsrc_t prs = __builtin_amdgcn_make_buffer_rsrc(
-      part, 0, (int)((uint32_t)(N / NC) * (uint32_t)ks_count * kSlotBytes), kBufferWord3);
+      part, 0, (int)((uint32_t)((N + NC - 1) / NC) * (uint32_t)ks_count * kSlotBytes), kBufferWord3);
   auto soff = [&](int q) { return (uint32_t)(cb * ks_count + q) * kSlotBytes + (uint32_t)wave * kWaveRegion; };
   const uint32_t vlane = (uint32_t)lane * 16;
   unsigned* cnt = counters + cb * kWaves + wave;
@@ -353,23 +359,24 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
   if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Workspace: a fixed 4 KB of (column block, wave) counters, then the
-// partials.  K is split only while the counters fit (pick_ks); they sit at
-// the same place for every shape, which keeps the library workspace clean
-// (all counters zero) from one call to the next whatever the shapes.
-// Unsplit shapes need no workspace.
-// Row blocks of the instance that serves M rows (even from 8 on: 2 x 2 waves).
 constexpr int kMaxRows = 256;
 
+// Row blocks of the instance that serves M rows (even from 8 on: 2 x 2 waves).
 int pick_mb(size_t m) {
   const int mb = (int)((m + 15) / 16);
   return mb > 8 ? (mb + 1) & ~1 : mb;
 }
 
+// Workspace: a fixed 4 KB of (column block, wave) counters, then the
+// partials.  K is split only while the counters fit (pick_ks); they sit at
+// the same place for every shape, which keeps the library workspace clean
+// (all counters zero) from one call to the next whatever the shapes.
+// Unsplit shapes need no workspace.
 size_t sk_workspace(size_t m, size_t n, size_t k, int num_cus) {
   const int ks = pick_ks(n, k, num_cus);
   if (ks == 1) return 0;
-  return kCounterBytes + (size_t)ks * n * 16 * pick_mb(m) * sizeof(float);
+  const size_t ncb = (n + pick_nc(n) - 1) / pick_nc(n);
+  return kCounterBytes + (size_t)ks * ncb * pick_nc(n) * 16 * pick_mb(m) * sizeof(float);
 }
 
 template <int NC, int MB, typename OutT>
@@ -383,7 +390,7 @@ hipError_t launch_sk_t(const GemmArgs& a) {
   unsigned* counters = nullptr;
   float* part = nullptr;
   if (ks > 1) {
-    if ((a.n / NC) * kWaves * sizeof(unsigned) > kCounterBytes) return hipErrorInvalidValue;
+    if (((a.n + NC - 1) / NC) * kWaves * sizeof(unsigned) > kCounterBytes) return hipErrorInvalidValue;
     counters = static_cast<unsigned*>(a.workspace);
     part = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + kCounterBytes);
     if (!a.workspace_clean) {
@@ -391,7 +398,7 @@ hipError_t launch_sk_t(const GemmArgs& a) {
       if (e != hipSuccess) return e;
     }
   }
-  const unsigned grid = (unsigned)((a.n / NC) * ks);
+  const unsigned grid = (unsigned)(((a.n + NC - 1) / NC) * ks);
   hipLaunchKernelGGL(kfn, dim3(grid), dim3(kThreads), G::kLdsBytes, a.stream, static_cast<const half_t*>(a.A),
                      static_cast<const half_t*>(a.B), static_cast<OutT*>(a.C), (int)a.m, (int)a.n, (int)a.k, ks,
                      part, counters);
@@ -425,12 +432,12 @@ hipError_t launch_sk(const GemmArgs& a) { return launch_nc<128>(a); }
 
 // Any M up to 256 (measured at N = K = 8192, µs per launch, this kernel
 // against the 256-row tiles of versions 10 / 9: M = 200 49.1 / 54.6, 224
-// 48.6 / 55.0, 256 53.2 / 54.7); N a multiple of 128; K a multiple of 32; the
+// 48.6 / 55.0, 256 53.2 / 54.7); N a multiple of 8; K a multiple of 32; the
 // 32-bit lane byte offsets into A (up to 256 rows) and B (32 rows) must not
 // overflow.
 bool sk_shape_ok(size_t m, size_t n, size_t k) {
   return m >= 1 && m <= kMaxRows && (size_t)256 * k * 2 < (1ull << 31) && (size_t)32 * n * 2 < (1ull << 31) &&
-         (n / 128) * 8 < (1ull << 31);
+         ((n + 127) / 128) * 8 < (1ull << 31);
 }
 
 }  // namespace
@@ -440,7 +447,7 @@ void register_f16_skinny_sk() {
   e.version = 8;
   e.in_dtype = VK_DTYPE_F16;
   e.name = "f16_v8_skinny_splitk";
-  e.caps = make_caps(8, VK_DTYPE_F16, kOutF16 | kOutF32, 1, 128, kKStep, 16, 256, 128, kKStep, kThreads,
+  e.caps = make_caps(8, VK_DTYPE_F16, kOutF16 | kOutF32, 1, 8, kKStep, 16, 256, 128, kKStep, kThreads,
                      SkCfg<128, 16>::kLdsBytes, 0, 1, kMaxRows);
   e.launch = launch_sk;
   e.workspace = sk_workspace;
