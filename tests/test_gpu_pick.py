@@ -48,3 +48,17 @@ def test_f32_pick_runs_and_matches(gpu, oracle, shape, expected):
     C64 = oracle.dgemm(A, B)
     bound = 2.0 * k * 2.0 ** -24 * (np.abs(A).astype(np.float64) @ np.abs(B).astype(np.float64))
     assert np.all(np.abs(C - C64) <= bound + 1e-30)
+
+
+def test_gemm_without_version_uses_the_pick(gpu, oracle):
+    """vibekernel_amd.gemm(A, B) with no version: the picked kernel, fp16 and
+    fp32 outputs, within the fp32 bound."""
+    import torch
+    import vibekernel_amd as vk
+    for m, n, k in [(1, 4000, 512), (300, 264, 72), (512, 512, 512)]:
+        A, B = make_inputs(m, n, k, "uniform", seed=m + n)
+        tA, tB = torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda()
+        C = vk.gemm(tA, tB, out_dtype=torch.float32)
+        torch.cuda.synchronize()
+        check_f32_out(C.cpu().numpy(), A, B, oracle.dgemm(A, B))
+        assert vk.gemm(tA, tB).dtype == torch.float16

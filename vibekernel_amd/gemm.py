@@ -69,14 +69,18 @@ def matmul(m: int, n: int, k: int, A, B, C, version: int, stream=None) -> None:
         raise VkError(st, f"matmul(version={version}, m={m}, n={n}, k={k})")
 
 
-def gemm(A, B, version: int, out_dtype=None, stream=None):
-    """Allocate C and run :func:`matmul`; A is (m, k), B is (k, n)."""
+def gemm(A, B, version: int | None = None, out_dtype=None, stream=None):
+    """Allocate C and run :func:`matmul`; A is (m, k), B is (k, n).  With no
+    version, :func:`pick_version` chooses one for the shape and dtypes."""
     torch = _torch()
     m, k = A.shape
     k2, n = B.shape
     if k != k2:
         raise VkError(-3, f"inner dimensions differ: {k} vs {k2}")
     C = torch.empty((m, n), dtype=out_dtype or A.dtype, device=A.device)
+    if version is None:
+        dt = "f16" if A.dtype == torch.float16 else "f32"
+        version = pick_version(m, n, k, dt, "f16" if C.dtype == torch.float16 else "f32")
     matmul(m, n, k, A, B, C, version, stream)
     return C
 
