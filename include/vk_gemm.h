@@ -41,7 +41,12 @@ extern "C" {
 
 typedef enum vk_dtype {
   VK_DTYPE_F16 = 1, /* IEEE binary16 ("float16_t" = half in the reference, system.hpp:29) */
-  VK_DTYPE_F32 = 2  /* IEEE binary32 ("float32_t", system.hpp:27) */
+  VK_DTYPE_F32 = 2, /* IEEE binary32 ("float32_t", system.hpp:27) */
+  /* Not dtypes: they make every int value a valid vk_dtype, so a bad value
+   * from a C caller is reported (VK_ERR_DTYPE / VK_ERR_VERSION) rather than
+   * being undefined behaviour in the C++ library. */
+  VK_DTYPE_INT_MIN_ = -2147483647 - 1,
+  VK_DTYPE_INT_MAX_ = 2147483647
 } vk_dtype;
 
 typedef enum vk_status {
@@ -81,13 +86,19 @@ typedef struct vk_caps {
  * vk_gemm_release() or process exit.  All calls of such versions on one
  * device share that workspace, so they must not run concurrently (issue them
  * on one stream, or order them); concurrent callers pass their own
- * workspaces to vk_gemm_ws. */
+ * workspaces to vk_gemm_ws.  Under stream capture a call that would use the
+ * library workspace returns VK_ERR_WORKSPACE (a captured graph would keep an
+ * address that a later call may free); capture such calls with vk_gemm_ws.
+ * Calls that need no workspace may be captured. */
 int vk_gemm(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, size_t n, size_t k,
             const void* A, const void* B, void* C, void* stream);
 
 /* Same, with a caller-owned device workspace of at least
  * vk_gemm_workspace_bytes() bytes (may be NULL when that is 0).  Never
- * allocates. */
+ * allocates.  Safe under stream capture: the counters the kernels share are
+ * cleared by a small kernel (not a memset) in every call, so each replay of a
+ * captured graph starts from zero; calls sharing one workspace must not
+ * overlap. */
 int vk_gemm_ws(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, size_t n, size_t k,
                const void* A, const void* B, void* C, void* workspace, size_t workspace_bytes,
                void* stream);

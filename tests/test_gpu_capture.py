@@ -1,0 +1,94 @@
+"""Stream capture (HIP graphs) of the C ABI: a split-tail call (version 10 on
+1000 x 1000 x 4000, whose tail tiles are cut into pieces that meet through a
+workspace) captured with a caller workspace (vk_gemm_ws) and replayed several
+times, with eager work and synchronisations between the replays, each replay
+bit-identical to the eager call and within the fp32 bound of the exact
+product; the same call through the library workspace (vk_gemm) is refused
+under capture; a version with no workspace captures through vk_gemm."""
+import numpy as np
+import pytest
+
+from gpu_util import announce, check_f16_out, make_inputs
+
+pytestmark = pytest.mark.gpu
+
+
+def _ptr(t):
+    import ctypes
+    return ctypes.c_void_p(t.data_ptr())
+
+
+def test_split_tail_capture_and_replay(gpu, oracle):
+    import torch
+    import vibekernel_amd as vk
+    from vibekernel_amd import _abi
+    m, n, k = 1000, 1000, 4000
+    A, B = make_inputs(m, n, k, "uniform", seed=31)
+    tA, tB = torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda()
+    need = _abi.workspace_bytes(10, vk.DTYPE_F16, m, n, k)
+    assert need > 0  # the plan splits this shape's tail
+    ws = torch.empty(need, dtype=torch.uint8, device="cuda:0")
+    C_eager = torch.full((m, n), float("nan"), dtype=torch.float16, device="cuda:0")
+    announce("capture: eager v10 1000x1000x4000 with caller workspace")
+    s = torch.cuda.current_stream()
+    st = _abi.gemm_ws(10, vk.DTYPE_F16, vk.DTYPE_F16, m, n, k, _ptr(tA), _ptr(tB), _ptr(C_eager),
+                      _ptr(ws), need, _ptr_stream(s))
+    assert st == 0
+    torch.cuda.synchronize()
+    ref = C_eager.cpu().numpy()
+    check_f16_out(ref, A, B, A.astype(np.float64) @ B.astype(np.float64))
+
+    C = torch.empty((m, n), dtype=torch.float16, device="cuda:0")
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            cs = torch.cuda.current_stream()
+            # the library workspace is refused under capture
+            st_lib = _abi.gemm(10, vk.DTYPE_F16, vk.DTYPE_F16, m, n, k, _ptr(tA), _ptr(tB), _ptr(C),
+                               _ptr_stream(cs))
+            st_ws = _abi.gemm_ws(10, vk.DTYPE_F16, vk.DTYPE_F16, m, n, k, _ptr(tA), _ptr(tB), _ptr(C),
+                                 _ptr(ws), need, _ptr_stream(cs))
+    torch.cuda.current_stream().wait_stream(side)
+    assert st_lib == -6 and st_ws == 0
+    for r in range(4):
+        C.fill_(float("nan"))
+        torch.matmul(tA[:64].float(), tB[:, :64].float())  # eager work between replays
+        torch.cuda.synchronize()
+        announce(f"capture: replay {r}")
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(C.cpu().numpy().view(np.uint16), ref.view(np.uint16)), f"replay {r}"
+
+
+def _ptr_stream(s):
+    import ctypes
+    return ctypes.c_void_p(s.cuda_stream)
+
+
+def test_no_workspace_version_captures_through_vk_gemm(gpu):
+    import torch
+    import vibekernel_amd as vk
+    from vibekernel_amd import _abi
+    m = n = k = 512
+    A, B = make_inputs(m, n, k, "int", seed=5)
+    tA, tB = torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda()
+    C = torch.empty((m, n), dtype=torch.float16, device="cuda:0")
+    g = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    announce("capture: v7 512^3 through vk_gemm")
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(g, stream=side):
+            st = _abi.gemm(7, vk.DTYPE_F16, vk.DTYPE_F16, m, n, k, _ptr(tA), _ptr(tB), _ptr(C),
+                           _ptr_stream(torch.cuda.current_stream()))
+    torch.cuda.current_stream().wait_stream(side)
+    assert st == 0
+    exact = (A.astype(np.int64) @ B.astype(np.int64)).astype(np.float16)
+    for _ in range(3):
+        C.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert np.array_equal(C.cpu().numpy().view(np.uint16), exact.view(np.uint16))

@@ -14,7 +14,6 @@
 #include <algorithm>
 #include <cstring>
 #include <mutex>
-#include <vector>
 
 #include "vk_device.hpp"
 #include "vk_gemm.h"
@@ -23,8 +22,16 @@
 namespace vk {
 namespace {
 
-std::vector<KernelEntry>& registry() {
-  static std::vector<KernelEntry> r;
+// The registered versions, in a fixed array: a lookup never allocates.
+constexpr int kMaxEntries = 32;
+struct Registry {
+  KernelEntry e[kMaxEntries];
+  int n = 0;
+  const KernelEntry* begin() const { return e; }
+  const KernelEntry* end() const { return e + n; }
+};
+Registry& registry() {
+  static Registry r;
   return r;
 }
 
@@ -54,15 +61,18 @@ size_t dtype_size(vk_dtype d) { return d == VK_DTYPE_F16 ? 2 : 4; }
 struct DeviceState {
   void* ws = nullptr;
   size_t ws_bytes = 0;
-  int ws_version = 0;  // version that used the library workspace last (0: none)
+  int ws_version = 0;  // version whose launch used the library workspace last (0: none)
   int num_cus = 0;
 };
+// One entry per device id, fixed in size: looking a device up never
+// allocates (host or device memory).
+constexpr int kMaxDevices = 64;
 std::mutex g_dev_mutex;
-std::vector<DeviceState> g_dev;
+DeviceState g_dev[kMaxDevices];
 
 hipError_t device_state(int dev, DeviceState** out) {
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
   std::lock_guard<std::mutex> lk(g_dev_mutex);
-  if ((int)g_dev.size() <= dev) g_dev.resize(dev + 1);
   DeviceState& s = g_dev[dev];
   if (s.num_cus == 0) {
     int cus = 0;
@@ -144,8 +154,16 @@ int run(int version, vk_dtype in, vk_dtype out, size_t m, size_t n, size_t k, co
 
   const size_t need = e->workspace ? e->workspace(m, n, k, ds->num_cus) : 0;
   bool ws_clean = false;
+  bool owns_ws = false;  // this call uses the library workspace
   if (need > 0) {
     if (library_ws) {
+      // A graph captured now would keep this workspace's address, which a
+      // later call may free and reallocate, and would replay the counter
+      // state decided here: under capture the library workspace is refused,
+      // and vk_gemm_ws (caller workspace) is the capture-safe form.
+      hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+      if (hipStreamIsCapturing(s, &cs) != hipSuccess) return VK_ERR_HIP;
+      if (cs != hipStreamCaptureStatusNone) return VK_ERR_WORKSPACE;
       std::lock_guard<std::mutex> lk(g_dev_mutex);
       if (ds->ws_bytes < need) {
         if (ds->ws) {
@@ -153,14 +171,18 @@ int run(int version, vk_dtype in, vk_dtype out, size_t m, size_t n, size_t k, co
           ds->ws = nullptr;
           ds->ws_bytes = 0;
         }
+        ds->ws_version = 0;
         if (hipMalloc(&ds->ws, need) != hipSuccess) return VK_ERR_HIP;
         ds->ws_bytes = need;
-        ds->ws_version = 0;
       }
       ws = ds->ws;
       ws_bytes = ds->ws_bytes;
       ws_clean = ds->ws_version == version;
-      ds->ws_version = version;
+      // Until this launch is known to have been enqueued, the counters count
+      // as unknown: a failed launch must not leave the next call skipping the
+      // clear.
+      ds->ws_version = 0;
+      owns_ws = true;
     } else if (!ws || ws_bytes < need) {
       return VK_ERR_WORKSPACE;
     }
@@ -180,12 +202,22 @@ int run(int version, vk_dtype in, vk_dtype out, size_t m, size_t n, size_t k, co
   a.stream = s;
   a.device = dev;
   a.num_cus = ds->num_cus;
-  return e->launch(a) == hipSuccess ? VK_OK : VK_ERR_HIP;
+  if (e->launch(a) != hipSuccess) return VK_ERR_HIP;
+  if (owns_ws) {
+    // The kernels of a version leave the counters they use at zero, so the
+    // next call of the same version may skip clearing them.
+    std::lock_guard<std::mutex> lk(g_dev_mutex);
+    if (ds->ws == ws) ds->ws_version = version;
+  }
+  return VK_OK;
 }
 
 }  // namespace
 
-void register_kernel(const KernelEntry& e) { registry().push_back(e); }
+void register_kernel(const KernelEntry& e) {
+  Registry& r = registry();
+  if (r.n < kMaxEntries) r.e[r.n++] = e;
+}
 
 }  // namespace vk
 
@@ -247,11 +279,12 @@ int vk_gemm_release(void) {
   int st = VK_OK;
   int cur = 0;
   if (hipGetDevice(&cur) != hipSuccess) return VK_ERR_HIP;
-  for (size_t d = 0; d < vk::g_dev.size(); d++) {
+  for (int d = 0; d < vk::kMaxDevices; d++) {
     if (!vk::g_dev[d].ws) continue;
-    if (hipSetDevice((int)d) != hipSuccess || hipFree(vk::g_dev[d].ws) != hipSuccess) st = VK_ERR_HIP;
+    if (hipSetDevice(d) != hipSuccess || hipFree(vk::g_dev[d].ws) != hipSuccess) st = VK_ERR_HIP;
     vk::g_dev[d].ws = nullptr;
     vk::g_dev[d].ws_bytes = 0;
+    vk::g_dev[d].ws_version = 0;
   }
   if (hipSetDevice(cur) != hipSuccess) st = VK_ERR_HIP;
   return st;
