@@ -58,7 +58,7 @@ private:
     DType* ptr_ = nullptr;
 };
 
-enum class Dist { Normal, Uniform, Normal05 };
+enum class Dist { Normal, Uniform, Normal05, Int };
 
 struct TestConfig {
     Dist dist = Dist::Normal;     // the reference draws N(0,1)
@@ -70,7 +70,8 @@ inline Dist parse_dist(const std::string& s) {
     if (s == "normal") return Dist::Normal;
     if (s == "uniform") return Dist::Uniform;
     if (s == "normal0.5") return Dist::Normal05;
-    throw std::invalid_argument("unknown distribution '" + s + "' (normal|uniform|normal0.5)");
+    if (s == "int") return Dist::Int;  // integers in [-2, 2]: exact products, and GT == 0 terms
+    throw std::invalid_argument("unknown distribution '" + s + "' (normal|uniform|normal0.5|int)");
 }
 
 class TestData {
@@ -97,6 +98,9 @@ public:
         auto fill = [&](std::vector<params::DataType>& v) {
             if (_cfg.dist == Dist::Uniform) {
                 std::uniform_real_distribution<float64_t> d(-1.0, 1.0);
+                for (auto& x : v) x = params::DataType(d(gen));
+            } else if (_cfg.dist == Dist::Int) {
+                std::uniform_int_distribution<int> d(-2, 2);
                 for (auto& x : v) x = params::DataType(d(gen));
             } else {
                 std::normal_distribution<float64_t> d(0.0, _cfg.dist == Dist::Normal ? 1.0 : 0.5);

@@ -43,6 +43,34 @@ int vkb_stream_loop(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m
                     size_t k, const void* A, const void* B, void* C, void* stream, int warmup,
                     int iters, float* total_ms);
 
+/* GPU clocks and socket power over a region, sampled on a host thread from
+ * the driver's metrics table (amd-smi; no GPU work is issued).  The table is
+ * refreshed about once per second, so only a region of a few seconds holds
+ * samples; the refreshes seen during the region count, the table as it stood
+ * when the region began does not.  SCLK is the mean over XCDs of
+ * current_gfxclks, averaged over those samples.  Not in the reference, whose
+ * post-mortem asks that every run log the clock (README.md:160 of the
+ * reference). */
+typedef struct vkb_clock_stats {
+  int samples;          /* distinct metric-table samples in the region */
+  double window_ms;     /* host time between start and stop */
+  double gfx_mhz_mean;  /* SCLK */
+  double gfx_mhz_min;
+  double gfx_mhz_max;
+  double uclk_mhz_mean; /* memory clock (0: not reported) */
+  double socket_w_mean; /* socket power in W (0: not reported) */
+  double gfx_activity_mean; /* GFX busy percentage (-1: not reported) */
+} vkb_clock_stats;
+
+/* Open the sampler for the current HIP device (VK_OK, or VK_ERR_HIP with the
+ * reason in vkb_clock_error()). */
+int vkb_clock_open(void);
+/* Start sampling every interval_us microseconds. */
+int vkb_clock_start(int interval_us);
+/* Stop and fill *out; VK_ERR_HIP when no sample was taken. */
+int vkb_clock_stop(vkb_clock_stats* out);
+const char* vkb_clock_error(void);
+
 #ifdef __cplusplus
 }
 #endif

@@ -153,11 +153,22 @@ def test_headline_4096_reference_metric(gpu, oracle, version):
     e_gpu, st1 = oracle.mean_rel_err(exact16, C)
     e_v0, st2 = oracle.mean_rel_err(exact16, GT)
     e_ref, st3 = oracle.mean_rel_err(GT, C)
-    assert st1 == st2 == st3 == oracle.STATUS_OK
-    print(f"v{version} 4096^3 N(0,1): mean-rel vs exact {e_gpu:.3e} (v0: {e_v0:.3e}); vs v0 {e_ref:.3e}")
+    # The reference's own ground truth is an OpenBLAS sgemm (blocked, not one
+    # sequential chain per element): numpy's bundled OpenBLAS on the widened
+    # inputs, narrowed with RNE, stands in for it.  Statistical, not bitwise.
+    GTb = (A.astype(np.float32) @ B.astype(np.float32)).astype(np.float16)
+    e_blas, st4 = oracle.mean_rel_err(GTb, C)
+    assert st1 == st2 == st3 == st4 == oracle.STATUS_OK
+    print(f"v{version} 4096^3 N(0,1): mean-rel vs exact {e_gpu:.3e} (v0: {e_v0:.3e}); vs v0 {e_ref:.3e}; "
+          f"vs OpenBLAS GT {e_blas:.3e} (the reference's strict tier on A100: 3.4e-5 to 4.6e-5)")
     assert e_gpu <= e_v0
     assert e_gpu < 1e-5
     assert e_ref < 3e-4
+    # Against a blocked-summation ground truth like the reference's, the
+    # statistic is an order of magnitude below the reference's strict tier
+    # (its best fp32-accumulate kernels logged 3.4e-5, results/ralph_loop_fable/
+    # result.csv:59-60).
+    assert e_blas < 1e-5
 
 
 @pytest.mark.slow

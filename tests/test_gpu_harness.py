@@ -71,3 +71,34 @@ def test_bench_loops(gpu):
     # an invalid call reports its status instead of launching
     bad = (3, vk.DTYPE_F16, vk.DTYPE_F16, 1000, n, k) + call[6:]
     assert L.vkb_reference_loop(*bad, 0, 1, per) == -3
+
+
+def test_task1_printed_error_equals_oracle_statistic(gpu, oracle, tmp_path):
+    """The 'Average Error' a GPU binary prints is the oracle's statistic of
+    the same GT and C (--dump writes them), bit for bit, and nonzero; GT is
+    the oracle's v0 result bit for bit; the --json line carries the clock
+    sampled over the timed loop, the CU count and the host cores."""
+    import json
+
+    import numpy as np
+
+    from gpu_util import check_f16_out
+    from test_stat_parity import _read_dump
+    dump = str(tmp_path / "v7.bin")
+    announce("task1_float16_v7 -m 512 -n 768 -k 1024 --dump")
+    p = subprocess.run([os.path.join(BIN, "task1_float16_v7"), "-m", "512", "-n", "768", "-k", "1024", "-w", "2",
+                        "-t", "20", "--json", "--dump", dump], capture_output=True, text=True, timeout=120)
+    assert p.returncode == 0, p.stderr
+    A, B, GT, C = _read_dump(dump)
+    assert np.array_equal(GT.view(np.uint16), oracle.hgemm(A, B).view(np.uint16))
+    exact = A.astype(np.float64) @ B.astype(np.float64)
+    check_f16_out(C, A, B, exact)
+    printed = np.float32(RESULT_RE.search(p.stdout).group("err"))
+    v, st = oracle.mean_rel_err(GT, C)
+    assert st == oracle.STATUS_OK and printed > 0
+    assert printed.view(np.uint32) == np.float32(v).view(np.uint32)
+    j = json.loads([ln for ln in p.stdout.splitlines() if ln.startswith("{")][0])
+    assert j["cus"] > 0 and j["host_cores"] > 0 and 0 < j["pct_peak"] < 100
+    clk = j["clock"]
+    print("task1 clock record:", clk)
+    assert clk is not None and ("error" in clk or (clk["sclk_mhz"] > 0 and 0 < clk["frac_clock"] <= 1.05))
