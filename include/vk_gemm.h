@@ -103,6 +103,25 @@ int vk_gemm_ws(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, siz
                const void* A, const void* B, void* C, void* workspace, size_t workspace_bytes,
                void* stream);
 
+/* Size of the device scratch array behind vk_gemm_noalloc: the largest
+ * workspace any version plans on a device of up to 256 CUs (version 9's 256
+ * split-tail pieces of 256 KiB plus their counters; version 8's split-K
+ * partials stay within 32 MiB), with room to spare. */
+#define VK_GEMM_SCRATCH_BYTES ((size_t)64 * 1024 * 1024 + (size_t)64 * 1024)
+
+/* Same as vk_gemm, but allocates nothing (no hipMalloc or hipFree, no host
+ * allocation): a version that needs a workspace uses the library's scratch
+ * array of VK_GEMM_SCRATCH_BYTES in device memory, one copy per device, which
+ * each device that runs the library holds until the process ends.  A plan
+ * needing more returns VK_ERR_WORKSPACE.  The counters in it are cleared by a
+ * small kernel in every call; every call on one device shares that device's
+ * scratch, so calls that overlap on one device race (issue them on one
+ * stream).  No counterpart in the reference: for callers that cannot
+ * allocate -- code under HIP graph capture, tight serving loops, harnesses
+ * that forbid hipMalloc. */
+int vk_gemm_noalloc(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, size_t n, size_t k,
+                    const void* A, const void* B, void* C, void* stream);
+
 /* Workspace bytes a call of this version and shape needs on the current
  * device (0: none).  Versions 8 and 9 depend on the device's compute-unit count;
  * with no device to ask, an MI355X's 256 CUs are assumed.  No counterpart in

@@ -33,6 +33,7 @@ STATUS_NAMES = {
 EXPORTED_SYMBOLS = (
     "vk_gemm",
     "vk_gemm_ws",
+    "vk_gemm_noalloc",
     "vk_gemm_workspace_bytes",
     "vk_gemm_name",
     "vk_gemm_query",
@@ -119,6 +120,8 @@ def load() -> ctypes.CDLL:
     L.vk_gemm.restype = ci
     L.vk_gemm_ws.argtypes = [ci, ci, ci, sz, sz, sz, vp, vp, vp, vp, sz, vp]
     L.vk_gemm_ws.restype = ci
+    L.vk_gemm_noalloc.argtypes = [ci, ci, ci, sz, sz, sz, vp, vp, vp, vp]
+    L.vk_gemm_noalloc.restype = ci
     L.vk_gemm_workspace_bytes.argtypes = [ci, ci, sz, sz, sz]
     L.vk_gemm_workspace_bytes.restype = sz
     L.vk_gemm_name.argtypes = [ci, ci]
@@ -194,6 +197,10 @@ def gemm_ws(version, in_dtype, out_dtype, m, n, k, a_ptr, b_ptr, c_ptr, ws_ptr, 
             stream=None) -> int:
     return int(load().vk_gemm_ws(version, in_dtype, out_dtype, m, n, k, a_ptr, b_ptr, c_ptr,
                                  ws_ptr, ws_bytes, stream))
+
+
+def gemm_noalloc(version, in_dtype, out_dtype, m, n, k, a_ptr, b_ptr, c_ptr, stream=None) -> int:
+    return int(load().vk_gemm_noalloc(version, in_dtype, out_dtype, m, n, k, a_ptr, b_ptr, c_ptr, stream))
 
 
 def workspace_bytes(version, in_dtype, m, n, k) -> int:

@@ -19,6 +19,14 @@
 #include "vk_gemm.h"
 #include "vk_internal.hpp"
 
+// Workspace of vk_gemm_noalloc: split-K / split-tail partials and their
+// arrival counters.  Each device that loads this library holds its own copy
+// until the process ends.  In host code this name is only a stand-in for the
+// symbol: the device address of a device's copy comes from
+// hipGetSymbolAddress (scratch_of below), and only that address is handed to
+// kernels.
+static __device__ __align__(256) unsigned char scratch[VK_GEMM_SCRATCH_BYTES];
+
 namespace vk {
 namespace {
 
@@ -63,6 +71,7 @@ struct DeviceState {
   size_t ws_bytes = 0;
   int ws_version = 0;  // version whose launch used the library workspace last (0: none)
   int num_cus = 0;
+  void* scratch = nullptr;  // this device's copy of `scratch` (vk_gemm_noalloc)
 };
 // One entry per device id, fixed in size: looking a device up never
 // allocates (host or device memory).
@@ -81,6 +90,23 @@ hipError_t device_state(int dev, DeviceState** out) {
     s.num_cus = cus;
   }
   *out = &s;
+  return hipSuccess;
+}
+
+// Device address of this device's copy of `scratch`, looked up once per
+// device with that device current.
+hipError_t scratch_of(int dev, void** out) {
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lk(g_dev_mutex);
+  DeviceState& s = g_dev[dev];
+  if (!s.scratch) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    s.scratch = p;
+  }
+  *out = s.scratch;
   return hipSuccess;
 }
 
@@ -233,6 +259,21 @@ int vk_gemm_ws(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, siz
                void* stream) {
   return vk::run(version, in_dtype, out_dtype, m, n, k, A, B, C, workspace, workspace_bytes, false,
                  stream);
+}
+
+int vk_gemm_noalloc(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, size_t n, size_t k,
+                    const void* A, const void* B, void* C, void* stream) {
+  const int st = vk::validate(vk::find(version, in_dtype), out_dtype, m, n, k, A, B, C);
+  if (st != VK_OK || m == 0 || n == 0 || k == 0)
+    return st != VK_OK ? st : vk::run(version, in_dtype, out_dtype, m, n, k, A, B, C, nullptr, 0, false, stream);
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return VK_ERR_HIP;
+  void* sp = nullptr;
+  if (vk::scratch_of(dev, &sp) != hipSuccess) return VK_ERR_HIP;
+  // A caller workspace of VK_GEMM_SCRATCH_BYTES: a plan that needs more is
+  // refused with VK_ERR_WORKSPACE, and the counters are cleared by a kernel
+  // in every call (the scratch keeps whatever the last call left).
+  return vk::run(version, in_dtype, out_dtype, m, n, k, A, B, C, sp, VK_GEMM_SCRATCH_BYTES, false, stream);
 }
 
 size_t vk_gemm_workspace_bytes(int version, vk_dtype in_dtype, size_t m, size_t n, size_t k) {
