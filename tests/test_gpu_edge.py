@@ -140,3 +140,34 @@ def test_split_caller_workspace(gpu):
         assert st == 0
         torch.cuda.synchronize()
         assert np.array_equal(tC.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("version,dtype", [(10, "f16"), (3, "f32")])
+@pytest.mark.parametrize("shape", [(3, 8, 72), (17, 40, 200), (300, 264, 104)])
+def test_memory_past_the_operands_is_never_read(gpu, version, dtype, shape):
+    """A and B are views at the start of larger buffers whose elements past
+    the matrices are +inf: the last k-tile's B rows past K and the A rows past
+    M lie beyond the allocations' matrix bytes, and the loads through buffer
+    resources sized to the matrices must return zeros there (K % 64 != 0 and
+    M, N off the tile grid).  Every C element is finite and exact."""
+    import torch
+    import vibekernel_amd as vk
+    m, n, k = shape
+    npdt = np.float16 if dtype == "f16" else np.float32
+    tdt = torch.float16 if dtype == "f16" else torch.float32
+    A, B = make_inputs(m, n, k, "int", seed=m + 3 * n + 5 * k, dtype=npdt)
+    pad = 1 << 16
+    bufA = torch.full((m * k + pad,), float("inf"), dtype=tdt, device="cuda:0")
+    bufB = torch.full((k * n + pad,), float("inf"), dtype=tdt, device="cuda:0")
+    bufA[:m * k] = torch.from_numpy(A.ravel()).cuda()
+    bufB[:k * n] = torch.from_numpy(B.ravel()).cuda()
+    tA = bufA[:m * k].view(m, k)
+    tB = bufB[:k * n].view(k, n)
+    C = torch.full((m, n), float("nan"), dtype=tdt, device="cuda:0")
+    announce(f"version={version} {dtype} inf past the operands m={m} n={n} k={k}")
+    vk.matmul(m, n, k, tA, tB, C, version)
+    torch.cuda.synchronize()
+    got = C.cpu().numpy().astype(np.float64)
+    exact = A.astype(np.float64) @ B.astype(np.float64)
+    assert np.all(np.isfinite(got))
+    assert np.array_equal(got, exact)

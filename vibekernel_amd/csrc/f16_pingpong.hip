@@ -61,12 +61,23 @@ constexpr int kVmWait = (kNS - 2) * kDma;
 static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
 static_assert(kLdsBytes >= 8 * 128 * 64 * 2, "fp16 epilogue staging: 16 KB per wave");
 
-// fp16 output block of one wave (128 x 64) staged in LDS: row pitch 128 B = 8
-// chunks of 16 B; physical chunk = chunk ^ ((row / 2) % 8).  Rows r and r+1
-// fall in different halves of the 256-byte bank space, so the 32 rows a
-// column-wise write touches spread over 16 distinct 16-byte slots.
-__device__ __forceinline__ uint32_t epi16_addr(uint32_t base, int row, int chunk) {
-  return base + row * 128 + 16 * (chunk ^ ((row >> 1) & 7));
+// fp16 output block of one wave (128 x 64) staged in LDS: row pitch 128 B =
+// 16 units of 8 B (4 halves); unit u of row r sits at unit u ^ (r % 16).
+// The MFMA lanes that write together hold the same 8-byte unit of 16
+// consecutive rows, which this spreads over all 16 unit positions of the
+// 128-byte row: measured on MI355X, the writes have no bank conflicts (the
+// previous layout, 16-byte chunks XOR (r / 2) % 8, cost 4 conflict cycles per
+// write instruction: all 262,144 of the 4096^3 kernel's conflict cycles).
+__device__ __forceinline__ uint32_t epi16_unit_addr(uint32_t base, int row, int unit) {
+  return base + row * 128 + 8 * (unit ^ (row & 15));
+}
+// The 16 bytes of units 2ch and 2ch+1 of a row: one 16-byte read at unit
+// pair ch ^ (r / 2) % 8, whose two halves come swapped when r is odd.  (Also
+// conflict-free, measured: 8 rows x 8 pairs per instruction.)
+__device__ __forceinline__ uint4v epi16_read_pair(uint32_t base, int row, int ch) {
+  const uint4v v = lds_read16(base + row * 128 + 16 * (ch ^ ((row >> 1) & 7)));
+  const bool odd = row & 1;
+  return uint4v{odd ? v[2] : v[0], odd ? v[3] : v[1], odd ? v[0] : v[2], odd ? v[1] : v[3]};
 }
 
 template <typename OutT>
@@ -84,14 +95,14 @@ epilogue_store(float16v (&acc)[4][2], uint32_t wbase, OutT* Cw, int N, int lane)
         const int row = i * 32 + r0;
         half4 h = {(half_t)acc[i][j][4 * g4 + 0], (half_t)acc[i][j][4 * g4 + 1],
                    (half_t)acc[i][j][4 * g4 + 2], (half_t)acc[i][j][4 * g4 + 3]};
-        lds_write8(epi16_addr(wbase, row, 4 * j + g4) + 8 * hsel, h);
+        lds_write8(epi16_unit_addr(wbase, row, 2 * (4 * j + g4) + hsel), h);
       }
   // Read back 8 rows x 8 chunks per instruction: each row a full 128-byte line.
   const int rsub = lane >> 3, ch = lane & 7;
 #pragma unroll
   for (int q = 0; q < 16; q++) {
     const int row = 8 * q + rsub;
-    const uint4v v = lds_read16(epi16_addr(wbase, row, ch));
+    const uint4v v = epi16_read_pair(wbase, row, ch);
     *reinterpret_cast<uint4v*>(Cw + (size_t)row * N + ch * 8) = v;
   }
 }
@@ -564,13 +575,14 @@ template <typename OutT>
 struct Epi16;
 
 // fp16: the whole 128x64 block fits the region (row pitch 128 B, see
-// epi16_addr), so only the second flush() stores, 8 rows x 8 chunks per read.
+// epi16_unit_addr), so only the second flush() stores, 8 rows x 8 chunks per
+// read.
 template <>
 struct Epi16<half_t> {
   static __device__ __forceinline__ void stage(uint32_t wbase, int lane, int i, int j, const float4v& v) {
     const int r0 = lane & 15, g = lane >> 4;
     half4 h = {(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
-    lds_write8(epi16_addr(wbase, i * 16 + r0, 2 * j + (g >> 1)) + 8 * (g & 1), h);
+    lds_write8(epi16_unit_addr(wbase, i * 16 + r0, 4 * j + g), h);
   }
   static __device__ __forceinline__ void flush(uint32_t wbase, half_t* Cw, int N, int lane, int half) {
     if (half == 0) return;
@@ -578,7 +590,7 @@ struct Epi16<half_t> {
 #pragma unroll
     for (int q = 0; q < 16; q++) {
       const int row = 8 * q + rsub;
-      const uint4v v = lds_read16(epi16_addr(wbase, row, ch));
+      const uint4v v = epi16_read_pair(wbase, row, ch);
       *reinterpret_cast<uint4v*>(Cw + (size_t)row * N + ch * 8) = v;
     }
   }
@@ -592,7 +604,7 @@ struct Epi16<half_t> {
 #pragma unroll
     for (int q = 0; q < 16; q++) {
       const int row = 8 * q + rsub;
-      const uint4v v = lds_read16(epi16_addr(wbase, row, ch));
+      const uint4v v = epi16_read_pair(wbase, row, ch);
       if (col_in && row0 + row < M) *reinterpret_cast<uint4v*>(C + (size_t)(row0 + row) * N + col0 + ch * 8) = v;
     }
   }
