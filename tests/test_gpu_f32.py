@@ -17,7 +17,8 @@ from gpu_util import announce, make_inputs
 
 pytestmark = pytest.mark.gpu
 
-SHAPES_V1 = [(128, 128, 16), (256, 384, 64), (512, 512, 512), (1, 1, 1), (17, 33, 65), (130, 250, 70)]
+SHAPES_V1 = [(128, 128, 16), (256, 384, 64), (512, 512, 512), (1, 1, 1), (17, 33, 65), (130, 250, 70),
+             (128, 256, 16), (256, 512, 32), (384, 768, 48), (1024, 512, 1024), (128, 256, 2000)]
 SHAPES_V2 = [(256, 256, 16), (512, 256, 64), (256, 512, 48), (768, 512, 256), (1024, 1024, 512)]
 SHAPES_V3 = [(1, 4, 4), (17, 36, 68), (300, 260, 100), (257, 512, 36), (1000, 1000, 1000), (256, 256, 64)]
 CASES = [(1, s) for s in SHAPES_V1] + [(2, s) for s in SHAPES_V2] + [(3, s) for s in SHAPES_V3]

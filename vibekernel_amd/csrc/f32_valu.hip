@@ -14,13 +14,15 @@
 //     one is multiplied, then written to the other LDS buffer (one barrier per
 //     k-tile); the k-steps are unrolled by 2, so the compiler keeps two
 //     k-steps of fragments live, not the whole k-tile.
-// Roofline: the VOP2 FMA (`v_fmac_f32_e32`, what this compiles to) runs at
-// the full 157.3 TFLOP/s rate on MI355X (measured 146.7 on independent
-// chains; the VOP3 form runs at half).  What limits the kernel is the LDS
-// return path: each 16-byte read returns 1 KB per wave whatever the
-// broadcast, so it is the reads per FMA that count: 6 per 128 FMAs here
-// (8x16 outputs) against 4 per 64 at 8x8 -- measured 91.0 against 82.9
-// TFLOP/s on one box.
+// Roofline: the VOP2 FMA (`v_fmac_f32_e32`) runs at the full 157.3 TFLOP/s
+// rate on MI355X (measured 146.7 on independent chains; the VOP3 form runs
+// at half), unless its three VGPR operands share a register bank, which
+// halves it.  Tile-divisible shapes run the asm k-loop below
+// (f32_valu_asm_kernel), whose register layout rules that out: 102.5 TFLOP/s
+// at 4096^3 against 92.3 for this C++ kernel (3 interleaved pairs, one box),
+// where the compiler had put a quarter of the FMAs' operands in one bank.
+// Both are power-limited (the board at its ~1.4 kW cap, SCLK 1.9 GHz for the
+// asm kernel).  Other shapes run the C++ kernel with bounds checks.
 #include "vk_device.hpp"
 #include "vk_internal.hpp"
 
@@ -151,6 +153,232 @@ __global__ __launch_bounds__(256) void f32_valu_kernel(const float* __restrict__
   }
 }
 
+// Every VGPR from v32 up: the registers the asm kernel below uses itself.
+#define VK_CLOBBER_V32_V255 \
+  "v32", "v33", "v34", "v35", "v36", "v37", "v38", "v39", "v40", "v41", "v42", "v43", "v44", "v45", "v46", \
+  "v47", "v48", "v49", "v50", "v51", "v52", "v53", "v54", "v55", "v56", "v57", "v58", "v59", "v60", "v61", \
+  "v62", "v63", "v64", "v65", "v66", "v67", "v68", "v69", "v70", "v71", "v72", "v73", "v74", "v75", "v76", \
+  "v77", "v78", "v79", "v80", "v81", "v82", "v83", "v84", "v85", "v86", "v87", "v88", "v89", "v90", "v91", \
+  "v92", "v93", "v94", "v95", "v96", "v97", "v98", "v99", "v100", "v101", "v102", "v103", "v104", "v105", \
+  "v106", "v107", "v108", "v109", "v110", "v111", "v112", "v113", "v114", "v115", "v116", "v117", "v118", \
+  "v119", "v120", "v121", "v122", "v123", "v124", "v125", "v126", "v127", "v128", "v129", "v130", "v131", \
+  "v132", "v133", "v134", "v135", "v136", "v137", "v138", "v139", "v140", "v141", "v142", "v143", "v144", \
+  "v145", "v146", "v147", "v148", "v149", "v150", "v151", "v152", "v153", "v154", "v155", "v156", "v157", \
+  "v158", "v159", "v160", "v161", "v162", "v163", "v164", "v165", "v166", "v167", "v168", "v169", "v170", \
+  "v171", "v172", "v173", "v174", "v175", "v176", "v177", "v178", "v179", "v180", "v181", "v182", "v183", \
+  "v184", "v185", "v186", "v187", "v188", "v189", "v190", "v191", "v192", "v193", "v194", "v195", "v196", \
+  "v197", "v198", "v199", "v200", "v201", "v202", "v203", "v204", "v205", "v206", "v207", "v208", "v209", \
+  "v210", "v211", "v212", "v213", "v214", "v215", "v216", "v217", "v218", "v219", "v220", "v221", "v222", \
+  "v223", "v224", "v225", "v226", "v227", "v228", "v229", "v230", "v231", "v232", "v233", "v234", "v235", \
+  "v236", "v237", "v238", "v239", "v240", "v241", "v242", "v243", "v244", "v245", "v246", "v247", "v248", \
+  "v249", "v250", "v251", "v252", "v253", "v254", "v255"
+
+// The asm kernel's 32-bit byte offsets: A's 128-row panel, B's 256-column
+// strip over all of K, and C's 128-row panel.
+bool asm_offsets_fit(size_t m, size_t n, size_t k) {
+  (void)m;
+  const uint64_t lim = 1ull << 32;
+  return 128ull * k * 4 < lim && (uint64_t)k * n * 4 < lim && 128ull * n * 4 < lim && n < (1ull << 31) &&
+         k < (1ull << 31);
+}
+
+// ---------------------------------------------------------------------------
+// Full tiles (M % 128, N % 256, K % 16 == 0, 16-byte aligned operands): the
+// same tile, thread mapping, LDS layout and summation order as the kernel
+// above, with the k-loop written as one asm block so that the registers are
+// chosen here rather than by the compiler.
+//
+// Why: a v_fmac_f32 whose three operands (accumulator, a, b) sit in the same
+// VGPR bank (register number mod 4) issues at half rate; with two in one
+// bank there is no measurable loss (microbenchmarks on MI355X: 63-70 against
+// 124-139 TFLOP/s).  For the C++ kernel the compiler put every accumulator in
+// its b operand's bank, and a quarter of the 256 FMAs of a k-step pair also
+// had a in that bank.  Here:
+//   acc[i][j]  v[128 + 16 i + ((j + 1) % 16)]   bank (j + 1) % 4
+//   b[j]       v[64 + j] / v[80 + j]            bank j % 4       (2 buffers)
+//   a[i]       v[96 + i] / v[104 + i]           bank i % 4       (2 buffers)
+// so an accumulator never shares b's bank, and no FMA has three operands in
+// one bank.  Prefetched global tiles: A v[112:119], B v[32:47]; the inputs
+// the compiler supplies live below v32 (every register from v32 up is
+// declared clobbered).  Each k-step issues the next k-step's six LDS reads
+// into the other buffer ahead of its 128 FMAs; a k-tile ends with the next
+// k-tile's stores into the other LDS buffer and one barrier, as above.
+// Each output is one v_fmac_f32 per k in ascending order from 0: the same
+// sums, bit for bit, as the C++ kernel and the oracle.
+__global__ __launch_bounds__(256) void f32_valu_asm_kernel(const float* __restrict__ A,
+                                                           const float* __restrict__ B, float* __restrict__ C,
+                                                           int N, int K) {
+  __shared__ __attribute__((aligned(16))) float As[2][kBK * kApitch];
+  __shared__ __attribute__((aligned(16))) float Bs[2][kBK * kTN];
+  const uint32_t tid = threadIdx.x;
+  const uint32_t tx = tid & 15, ty = tid >> 4;
+  const size_t m0 = (size_t)blockIdx.y * kTM, n0 = (size_t)blockIdx.x * kTN;
+  const char* abase = reinterpret_cast<const char*>(A + m0 * (size_t)K);
+  const char* bbase = reinterpret_cast<const char*>(B + n0);
+  char* cbase = reinterpret_cast<char*>(C + m0 * (size_t)N + n0);
+  // Global byte offsets of this thread's float4 loads within the k-tile:
+  // A rows tid/4 and tid/4 + 64 at column (tid % 4) * 4; B k-rows tid/64 + 4e
+  // at column (tid % 64) * 4.  They advance by one k-tile per tile.
+  uint32_t ga0 = ((tid >> 2) * (uint32_t)K + (tid & 3) * 4) * 4;
+  uint32_t ga1 = ga0 + 64u * (uint32_t)K * 4;
+  uint32_t gb0 = ((tid >> 6) * (uint32_t)N + (tid & 63) * 4) * 4;
+  uint32_t gb1 = gb0 + 4u * (uint32_t)N * 4, gb2 = gb1 + 4u * (uint32_t)N * 4, gb3 = gb2 + 4u * (uint32_t)N * 4;
+  const uint32_t astep = kBK * 4, bstep = (uint32_t)kBK * (uint32_t)N * 4;
+  // LDS byte addresses for buffer 0 and the sum of the buffer-0 and buffer-1
+  // addresses, so that addr = sum - addr switches buffers.
+  const uint32_t as0 = lds_addr32(As[0]), as1 = lds_addr32(As[1]);
+  const uint32_t bs0 = lds_addr32(Bs[0]), bs1 = lds_addr32(Bs[1]);
+  uint32_t rd_a = as0 + ty * 16, rd_b = bs0 + tx * 16;                       // reads
+  uint32_t wr_a = as0 + ((tid & 3) * 4 * kApitch + (tid >> 2)) * 4;           // transposed A stores
+  uint32_t wr_b = bs0 + ((tid >> 6) * kTN + (tid & 63) * 4) * 4;              // B stores
+  const uint32_t sum_a = as0 + as1 + 2 * (ty * 16), sum_b = bs0 + bs1 + 2 * (tx * 16);
+  const uint32_t sum_wa = as0 + as1 + 2 * (((tid & 3) * 4 * kApitch + (tid >> 2)) * 4);
+  const uint32_t sum_wb = bs0 + bs1 + 2 * (((tid >> 6) * kTN + (tid & 63) * 4) * 4);
+  // C: rows ty*4 + i (i < 4) and 64 + ty*4 + i - 4, columns 64 g + tx*4.
+  uint32_t c_lo = ((ty * 4) * (uint32_t)N + tx * 4) * 4;
+  uint32_t c_hi = c_lo + 64u * (uint32_t)N * 4;
+  const uint32_t crow = (uint32_t)N * 4;
+  uint32_t nk = (uint32_t)K / kBK;
+
+  asm volatile(
+      // Read k-step KK of the current LDS buffer into a-buffer AB, b-buffer BB.
+      ".macro VK_RD KK, AB, BB\n"
+      "  ds_read_b128 v[\\AB:\\AB+3], %[rd_a] offset:(\\KK*528)\n"
+      "  ds_read_b128 v[\\AB+4:\\AB+7], %[rd_a] offset:(\\KK*528+256)\n"
+      "  ds_read_b128 v[\\BB:\\BB+3], %[rd_b] offset:(\\KK*1024)\n"
+      "  ds_read_b128 v[\\BB+4:\\BB+7], %[rd_b] offset:(\\KK*1024+256)\n"
+      "  ds_read_b128 v[\\BB+8:\\BB+11], %[rd_b] offset:(\\KK*1024+512)\n"
+      "  ds_read_b128 v[\\BB+12:\\BB+15], %[rd_b] offset:(\\KK*1024+768)\n"
+      ".endm\n"
+      // 128 FMAs of one k-step on buffers AB, BB.
+      ".macro VK_FMA AB, BB\n"
+      "  .irp i, 0,1,2,3,4,5,6,7\n"
+      "  .irp j, 0,1,2,3,4,5,6,7,8,9,10,11,12,13,14,15\n"
+      "  v_fmac_f32 v[128+16*\\i+((\\j+1)&15)], v[\\AB+\\i], v[\\BB+\\j]\n"
+      "  .endr\n"
+      "  .endr\n"
+      ".endm\n"
+      // Global loads of the k-tile at the current offsets into A v[112:119], B v[32:47].
+      ".macro VK_GLD\n"
+      "  global_load_dwordx4 v[112:115], %[ga0], %[abase]\n"
+      "  global_load_dwordx4 v[116:119], %[ga1], %[abase]\n"
+      "  global_load_dwordx4 v[32:35], %[gb0], %[bbase]\n"
+      "  global_load_dwordx4 v[36:39], %[gb1], %[bbase]\n"
+      "  global_load_dwordx4 v[40:43], %[gb2], %[bbase]\n"
+      "  global_load_dwordx4 v[44:47], %[gb3], %[bbase]\n"
+      ".endm\n"
+      // Store the prefetched k-tile into the LDS buffer the write addresses name.
+      ".macro VK_ST\n"
+      "  .irp e, 0,1\n"
+      "  .irp q, 0,1,2,3\n"
+      "  ds_write_b32 %[wr_a], v[112+4*\\e+\\q] offset:(\\q*528+\\e*256)\n"
+      "  .endr\n"
+      "  .endr\n"
+      "  .irp e, 0,1,2,3\n"
+      "  ds_write_b128 %[wr_b], v[32+4*\\e:35+4*\\e] offset:(\\e*4096)\n"
+      "  .endr\n"
+      ".endm\n"
+      ".macro VK_ADV\n"
+      "  v_add_u32 %[ga0], %[astep], %[ga0]\n"
+      "  v_add_u32 %[ga1], %[astep], %[ga1]\n"
+      "  v_add_u32 %[gb0], %[bstep], %[gb0]\n"
+      "  v_add_u32 %[gb1], %[bstep], %[gb1]\n"
+      "  v_add_u32 %[gb2], %[bstep], %[gb2]\n"
+      "  v_add_u32 %[gb3], %[bstep], %[gb3]\n"
+      ".endm\n"
+      // accumulators = 0
+      "  .irp r, 0,16,32,48,64,80,96,112\n"
+      "  .irp c, 0,1,2,3,4,5,6,7,8,9,10,11,12,13,14,15\n"
+      "  v_mov_b32 v[128+\\r+\\c], 0\n"
+      "  .endr\n"
+      "  .endr\n"
+      // prologue: k-tile 0 into LDS buffer 0, then the write addresses move
+      // to buffer 1 and k-step 0 is read
+      "  VK_GLD\n"
+      "  VK_ADV\n"
+      "  s_waitcnt vmcnt(0)\n"
+      "  VK_ST\n"
+      "  v_sub_u32 %[wr_a], %[sum_wa], %[wr_a]\n"
+      "  v_sub_u32 %[wr_b], %[sum_wb], %[wr_b]\n"
+      "  s_waitcnt lgkmcnt(0)\n"
+      "  s_barrier\n"
+      "  VK_RD 0, 96, 64\n"
+      "L_vk_tile_%=:\n"
+      "  s_cmp_gt_u32 %[nk], 1\n"
+      "  s_cbranch_scc0 L_vk_noload_%=\n"
+      "  VK_GLD\n"
+      "  VK_ADV\n"
+      "L_vk_noload_%=:\n"
+      "  s_waitcnt lgkmcnt(0)\n"
+      // k-steps 0..13 in pairs, then 14 and 15
+      "  .irp kk, 0,2,4,6,8,10,12\n"
+      "  VK_RD (\\kk+1), 104, 80\n"
+      "  VK_FMA 96, 64\n"
+      "  s_waitcnt lgkmcnt(0)\n"
+      "  VK_RD (\\kk+2), 96, 64\n"
+      "  VK_FMA 104, 80\n"
+      "  s_waitcnt lgkmcnt(0)\n"
+      "  .endr\n"
+      "  VK_RD 15, 104, 80\n"
+      "  VK_FMA 96, 64\n"
+      "  s_waitcnt lgkmcnt(0)\n"
+      "  VK_FMA 104, 80\n"
+      "  s_cmp_gt_u32 %[nk], 1\n"
+      "  s_cbranch_scc0 L_vk_done_%=\n"
+      // next k-tile: store it into the other LDS buffer, barrier, switch the
+      // read and write buffers, read its k-step 0
+      "  s_waitcnt vmcnt(0)\n"
+      "  VK_ST\n"
+      "  v_sub_u32 %[wr_a], %[sum_wa], %[wr_a]\n"
+      "  v_sub_u32 %[wr_b], %[sum_wb], %[wr_b]\n"
+      "  v_sub_u32 %[rd_a], %[sum_a], %[rd_a]\n"
+      "  v_sub_u32 %[rd_b], %[sum_b], %[rd_b]\n"
+      "  s_waitcnt lgkmcnt(0)\n"
+      "  s_barrier\n"
+      "  s_nop 1\n"
+      "  VK_RD 0, 96, 64\n"
+      "  s_sub_u32 %[nk], %[nk], 1\n"
+      "  s_branch L_vk_tile_%=\n"
+      "L_vk_done_%=:\n"
+      // C: each row's 16 accumulators are gathered in column order into
+      // v[48:127] (4 rows at a time) and stored as 4 x 16 bytes per row
+      "  .irp half, 0,1\n"
+      "  .irp i, 0,1,2,3\n"
+      "  .irp j, 0,1,2,3,4,5,6,7,8,9,10,11,12,13,14,15\n"
+      "  v_mov_b32 v[48+16*\\i+\\j], v[128+16*(4*\\half+\\i)+((\\j+1)&15)]\n"
+      "  .endr\n"
+      "  .endr\n"
+      "  s_nop 4\n"
+      "  .irp i, 0,1,2,3\n"
+      "  .irp g, 0,1,2,3\n"
+      "  .if \\half == 0\n"
+      "  global_store_dwordx4 %[c_lo], v[48+16*\\i+4*\\g:51+16*\\i+4*\\g], %[cbase] offset:(\\g*256)\n"
+      "  .else\n"
+      "  global_store_dwordx4 %[c_hi], v[48+16*\\i+4*\\g:51+16*\\i+4*\\g], %[cbase] offset:(\\g*256)\n"
+      "  .endif\n"
+      "  .endr\n"
+      "  .if \\half == 0\n"
+      "  v_add_u32 %[c_lo], %[crow], %[c_lo]\n"
+      "  .else\n"
+      "  v_add_u32 %[c_hi], %[crow], %[c_hi]\n"
+      "  .endif\n"
+      "  s_nop 1\n"
+      "  .endr\n"
+      "  s_waitcnt vmcnt(0)\n"
+      "  .endr\n"
+      ".purgem VK_RD\n"
+      ".purgem VK_FMA\n"
+      ".purgem VK_GLD\n"
+      ".purgem VK_ST\n"
+      ".purgem VK_ADV\n"
+      : [ga0] "+v"(ga0), [ga1] "+v"(ga1), [gb0] "+v"(gb0), [gb1] "+v"(gb1), [gb2] "+v"(gb2), [gb3] "+v"(gb3),
+        [rd_a] "+v"(rd_a), [rd_b] "+v"(rd_b), [wr_a] "+v"(wr_a), [wr_b] "+v"(wr_b), [c_lo] "+v"(c_lo),
+        [c_hi] "+v"(c_hi), [nk] "+s"(nk)
+      : [abase] "s"(abase), [bbase] "s"(bbase), [cbase] "s"(cbase), [astep] "s"(astep), [bstep] "s"(bstep),
+        [crow] "s"(crow), [sum_a] "v"(sum_a), [sum_b] "v"(sum_b), [sum_wa] "v"(sum_wa), [sum_wb] "v"(sum_wb)
+      : "memory", VK_CLOBBER_V32_V255);
+}
+
 hipError_t launch_f32(const GemmArgs& a) {
   dim3 grid((unsigned)((a.n + kTN - 1) / kTN), (unsigned)((a.m + kTM - 1) / kTM));
   const float* A = static_cast<const float*>(a.A);
@@ -158,10 +386,9 @@ hipError_t launch_f32(const GemmArgs& a) {
   float* C = static_cast<float*>(a.C);
   const bool full = a.m % kTM == 0 && a.n % kTN == 0 && a.k % kBK == 0 &&
                     ((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 &&
-                    ((uintptr_t)C & 15) == 0;
+                    ((uintptr_t)C & 15) == 0 && asm_offsets_fit(a.m, a.n, a.k);
   if (full)
-    hipLaunchKernelGGL(f32_valu_kernel<false>, grid, dim3(256), 0, a.stream, A, B, C, (int64_t)a.m,
-                       (int64_t)a.n, (int64_t)a.k);
+    hipLaunchKernelGGL(f32_valu_asm_kernel, grid, dim3(256), 0, a.stream, A, B, C, (int)a.n, (int)a.k);
   else
     hipLaunchKernelGGL(f32_valu_kernel<true>, grid, dim3(256), 0, a.stream, A, B, C, (int64_t)a.m,
                        (int64_t)a.n, (int64_t)a.k);
