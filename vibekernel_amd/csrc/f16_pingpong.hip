@@ -741,8 +741,8 @@ __device__ __forceinline__ void pp16_mainloop(const half_t* __restrict__ A, cons
 
   // Scalar operands of the 8 loads of one k-tile.  The loop computes them in
   // the memory phase, before the phase barrier, so that the compute phase
-  // issues each load as two instructions (M0 and the load) between two
-  // MFMAs: a wave issues at most one instruction every 4 cycles, so the ~10
+  // issues each load as three instructions (M0, its wait state and the load)
+  // between two MFMAs: a wave issues at most one instruction every 4 cycles, so the ~10
   // scalar instructions of an address computation in front of a load leave
   // the matrix pipe idle for most of their length (measured: compute phases
   // of 1180 cycles for 1024 cycles of MFMA issue).

@@ -3,26 +3,23 @@
 // The reference has the fp32 harness path (results/naive_cycle4/include/
 // playground/system.hpp:35-41, results/naive_fable_cycle2/src/CMakeLists.txt:5-11)
 // and its v0 ground truth (matmul_f32_v0_cblas.cpp:8-12) but no hand-written
-// fp32 kernel; its only GPU fp32 version called cublasSgemm.  This is a
-// register-blocked VALU kernel:
+// fp32 kernel; its only GPU fp32 version called cublasSgemm.  Two
+// register-blocked VALU kernels share one tile and thread mapping:
 //   * 128x256 workgroup tile, BK = 16, 256 threads, 8x16 outputs per thread
 //     held as 4x4 register blocks (rows ty*4 and 64+ty*4, columns
 //     64*g + tx*4 for g = 0..3) so the LDS operand reads are 16-byte and
-//     conflict-free;
-//   * A is stored k-major in LDS (transposed on the store) and B as loaded;
-//   * the next k-tile is prefetched from HBM into registers while the current
-//     one is multiplied, then written to the other LDS buffer (one barrier per
-//     k-tile); the k-steps are unrolled by 2, so the compiler keeps two
-//     k-steps of fragments live, not the whole k-tile.
+//     conflict-free; one barrier per k-tile over two LDS buffers;
+//   * tile-divisible shapes: the k-loop as one asm block with hand-chosen
+//     registers, k-tiles staged by direct-to-LDS loads (f32_valu_asm_kernel);
+//   * any other shape: a C++ kernel with bounds checks, the next k-tile
+//     prefetched into registers and stored into LDS (A transposed, k-major).
 // Roofline: the VOP2 FMA (`v_fmac_f32_e32`) runs at the full 157.3 TFLOP/s
 // rate on MI355X (measured 146.7 on independent chains; the VOP3 form runs
 // at half), unless its three VGPR operands share a register bank, which
-// halves it.  Tile-divisible shapes run the asm k-loop below
-// (f32_valu_asm_kernel), whose register layout rules that out: 102.5 TFLOP/s
-// at 4096^3 against 92.3 for this C++ kernel (3 interleaved pairs, one box),
-// where the compiler had put a quarter of the FMAs' operands in one bank.
-// Both are power-limited (the board at its ~1.4 kW cap, SCLK 1.9 GHz for the
-// asm kernel).  Other shapes run the C++ kernel with bounds checks.
+// halves it.  The asm kernel's register layout rules that out: 106.0 TFLOP/s
+// at 4096^3 against 92.3 for the C++ kernel, where the compiler had put a
+// quarter of the FMAs' operands in one bank.  Both are power-limited (the
+// board at its ~1.4 kW cap, SCLK 1.9 GHz for the asm kernel).
 #include "vk_device.hpp"
 #include "vk_internal.hpp"
 
@@ -183,100 +180,100 @@ bool asm_offsets_fit(size_t m, size_t n, size_t k) {
 }
 
 // ---------------------------------------------------------------------------
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 // Full tiles (M % 128, N % 256, K % 16 == 0, 16-byte aligned operands): the
-// same tile, thread mapping, LDS layout and summation order as the kernel
-// above, with the k-loop written as one asm block so that the registers are
-// chosen here rather than by the compiler.
+// same tile, thread mapping and summation order as the kernel above, with
+// the k-loop written as one asm block so that the registers are chosen here
+// rather than by the compiler, and the k-tiles staged by direct-to-LDS loads.
 //
-// Why: a v_fmac_f32 whose three operands (accumulator, a, b) sit in the same
-// VGPR bank (register number mod 4) issues at half rate; with two in one
-// bank there is no measurable loss (microbenchmarks on MI355X: 63-70 against
-// 124-139 TFLOP/s).  For the C++ kernel the compiler put every accumulator in
-// its b operand's bank, and a quarter of the 256 FMAs of a k-step pair also
-// had a in that bank.  Here:
+// Registers.  A v_fmac_f32 whose three operands (accumulator, a, b) sit in
+// the same VGPR bank (register number mod 4) issues at half rate; with two in
+// one bank there is no measurable loss (microbenchmarks on MI355X: 63-70
+// against 124-139 TFLOP/s).  For the C++ kernel the compiler put every
+// accumulator in its b operand's bank, and a quarter of the 256 FMAs of a
+// k-step pair also had a in that bank.  Here:
 //   acc[i][j]  v[128 + 16 i + ((j + 1) % 16)]   bank (j + 1) % 4
-//   b[j]       v[64 + j] / v[80 + j]            bank j % 4       (2 buffers)
-//   a[i]       v[96 + i] / v[104 + i]           bank i % 4       (2 buffers)
-// so an accumulator never shares b's bank, and no FMA has three operands in
-// one bank.  Prefetched global tiles: A v[112:119], B v[32:47]; the inputs
-// the compiler supplies live below v32 (every register from v32 up is
-// declared clobbered).  Each k-step issues the next k-step's six LDS reads
-// into the other buffer ahead of its 128 FMAs; a k-tile ends with the next
-// k-tile's stores into the other LDS buffer and one barrier, as above.
+//   b[j]       v[64 + j] / v[80 + j]            bank j % 4  (2 buffers, one k-step)
+//   a          v[32:63] / v[96:127]             (2 buffers, 4 k-steps)
+// so an accumulator never shares b's bank and no FMA has three operands in
+// one bank.  The inputs the compiler supplies live below v32 (every register
+// from v32 up is declared clobbered).
+//
+// Staging.  Each wave issues 6 direct-to-LDS loads per k-tile (2 x 16 rows
+// of A, 4 k-rows of B) into the other of two LDS buffers right after the
+// barrier that freed it, and waits for its own loads (vmcnt) before the next
+// barrier: no staging VGPRs and no LDS stores.  A is kept row-major in LDS
+// (row pitch 64 B = 4 chunks of 16 B = 4 k), chunk ^ ((row / 4) % 4), so
+// the rows ty*4 + i of the four ty of a wave fall in four distinct chunks;
+// B as loaded (k-row pitch 1 KB).  One ds_read_b128 of A gives a thread four
+// consecutive k of one row, so A is read per group of 4 k-steps (8 reads:
+// rows ty*4 + i and 64 + ty*4 + i) into a[i][kk] = v[AQ + 4 i + kk % 4]; each
+// k-step issues the next k-step's four B reads (and, before a group's last
+// k-step, the next group's 8 A reads) into the other buffers ahead of its
+// 128 FMAs.  Measured on MI355X at 4096^3 (interleaved, 3 pairs, one box):
+// 1296.5 us against 1310.4 us for the same k-loop staged through registers
+// with A transposed by 4-byte LDS stores (106.0 against 104.9 TFLOP/s).
 // Each output is one v_fmac_f32 per k in ascending order from 0: the same
 // sums, bit for bit, as the C++ kernel and the oracle.
 __global__ __launch_bounds__(256) void f32_valu_asm_kernel(const float* __restrict__ A,
                                                            const float* __restrict__ B, float* __restrict__ C,
                                                            int N, int K) {
-  __shared__ __attribute__((aligned(16))) float As[2][kBK * kApitch];
-  __shared__ __attribute__((aligned(16))) float Bs[2][kBK * kTN];
+  __shared__ __attribute__((aligned(1024))) float As[2][kTM * kBK];
+  __shared__ __attribute__((aligned(1024))) float Bs[2][kBK * kTN];
   const uint32_t tid = threadIdx.x;
-  const uint32_t tx = tid & 15, ty = tid >> 4;
+  const uint32_t tx = tid & 15, ty = tid >> 4, lane = tid & 63;
+  const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const size_t m0 = (size_t)blockIdx.y * kTM, n0 = (size_t)blockIdx.x * kTN;
   const char* abase = reinterpret_cast<const char*>(A + m0 * (size_t)K);
   const char* bbase = reinterpret_cast<const char*>(B + n0);
   char* cbase = reinterpret_cast<char*>(C + m0 * (size_t)N + n0);
-  // Global byte offsets of this thread's float4 loads within the k-tile:
-  // A rows tid/4 and tid/4 + 64 at column (tid % 4) * 4; B k-rows tid/64 + 4e
-  // at column (tid % 64) * 4.  They advance by one k-tile per tile.
-  uint32_t ga0 = ((tid >> 2) * (uint32_t)K + (tid & 3) * 4) * 4;
-  uint32_t ga1 = ga0 + 64u * (uint32_t)K * 4;
-  uint32_t gb0 = ((tid >> 6) * (uint32_t)N + (tid & 63) * 4) * 4;
+  // Loads: A instruction e covers rows 32w + 16e + lane/4, the lane's 16 B
+  // landing at chunk position lane % 4, which holds k-chunk
+  // (lane % 4) ^ ((row / 4) % 4); B instruction e covers k-row w + 4e.
+  const uint32_t arow0 = 32 * w + (lane >> 2), arow1 = arow0 + 16;
+  uint32_t ga0 = (arow0 * (uint32_t)K + 4 * ((lane & 3) ^ ((arow0 >> 2) & 3))) * 4;
+  uint32_t ga1 = (arow1 * (uint32_t)K + 4 * ((lane & 3) ^ ((arow1 >> 2) & 3))) * 4;
+  uint32_t gb0 = (w * (uint32_t)N + lane * 4) * 4;
   uint32_t gb1 = gb0 + 4u * (uint32_t)N * 4, gb2 = gb1 + 4u * (uint32_t)N * 4, gb3 = gb2 + 4u * (uint32_t)N * 4;
   const uint32_t astep = kBK * 4, bstep = (uint32_t)kBK * (uint32_t)N * 4;
-  // LDS byte addresses for buffer 0 and the sum of the buffer-0 and buffer-1
-  // addresses, so that addr = sum - addr switches buffers.
   const uint32_t as0 = lds_addr32(As[0]), as1 = lds_addr32(As[1]);
   const uint32_t bs0 = lds_addr32(Bs[0]), bs1 = lds_addr32(Bs[1]);
-  uint32_t rd_a = as0 + ty * 16, rd_b = bs0 + tx * 16;                       // reads
-  uint32_t wr_a = as0 + ((tid & 3) * 4 * kApitch + (tid >> 2)) * 4;           // transposed A stores
-  uint32_t wr_b = bs0 + ((tid >> 6) * kTN + (tid & 63) * 4) * 4;              // B stores
-  const uint32_t sum_a = as0 + as1 + 2 * (ty * 16), sum_b = bs0 + bs1 + 2 * (tx * 16);
-  const uint32_t sum_wa = as0 + as1 + 2 * (((tid & 3) * 4 * kApitch + (tid >> 2)) * 4);
-  const uint32_t sum_wb = bs0 + bs1 + 2 * (((tid >> 6) * kTN + (tid & 63) * 4) * 4);
-  // C: rows ty*4 + i (i < 4) and 64 + ty*4 + i - 4, columns 64 g + tx*4.
+  // LDS destinations of this wave's loads (wave-uniform) and their sums over
+  // the two buffers, so that dst = sum - dst switches buffers.
+  uint32_t a_dst = as0 + w * 2048, b_dst = bs0 + w * 1024;
+  const uint32_t sa_dst = as0 + as1 + 2 * w * 2048, sb_dst = bs0 + bs1 + 2 * w * 1024;
+  // Reads: A at rd_a ^ 16 c for k-chunk c (rd_a's bits 4-5 hold (ty % 4) * 16
+  // over a 256-aligned row-block base), rows by immediate offsets.
+  uint32_t rd_a = as0 + ty * 256 + 16 * (ty & 3), rd_b = bs0 + tx * 16;
+  const uint32_t sum_a = as0 + as1 + 2 * (ty * 256 + 16 * (ty & 3)), sum_b = bs0 + bs1 + 2 * (tx * 16);
   uint32_t c_lo = ((ty * 4) * (uint32_t)N + tx * 4) * 4;
   uint32_t c_hi = c_lo + 64u * (uint32_t)N * 4;
   const uint32_t crow = (uint32_t)N * 4;
   uint32_t nk = (uint32_t)K / kBK;
+  uint32_t tmp;
 
   asm volatile(
-      // Read k-step KK of the current LDS buffer into a-buffer AB, b-buffer BB.
-      ".macro VK_RD KK, AB, BB\n"
-      "  ds_read_b128 v[\\AB:\\AB+3], %[rd_a] offset:(\\KK*528)\n"
-      "  ds_read_b128 v[\\AB+4:\\AB+7], %[rd_a] offset:(\\KK*528+256)\n"
-      "  ds_read_b128 v[\\BB:\\BB+3], %[rd_b] offset:(\\KK*1024)\n"
-      "  ds_read_b128 v[\\BB+4:\\BB+7], %[rd_b] offset:(\\KK*1024+256)\n"
-      "  ds_read_b128 v[\\BB+8:\\BB+11], %[rd_b] offset:(\\KK*1024+512)\n"
-      "  ds_read_b128 v[\\BB+12:\\BB+15], %[rd_b] offset:(\\KK*1024+768)\n"
-      ".endm\n"
-      // 128 FMAs of one k-step on buffers AB, BB.
-      ".macro VK_FMA AB, BB\n"
-      "  .irp i, 0,1,2,3,4,5,6,7\n"
-      "  .irp j, 0,1,2,3,4,5,6,7,8,9,10,11,12,13,14,15\n"
-      "  v_fmac_f32 v[128+16*\\i+((\\j+1)&15)], v[\\AB+\\i], v[\\BB+\\j]\n"
-      "  .endr\n"
-      "  .endr\n"
-      ".endm\n"
-      // Global loads of the k-tile at the current offsets into A v[112:119], B v[32:47].
-      ".macro VK_GLD\n"
-      "  global_load_dwordx4 v[112:115], %[ga0], %[abase]\n"
-      "  global_load_dwordx4 v[116:119], %[ga1], %[abase]\n"
-      "  global_load_dwordx4 v[32:35], %[gb0], %[bbase]\n"
-      "  global_load_dwordx4 v[36:39], %[gb1], %[bbase]\n"
-      "  global_load_dwordx4 v[40:43], %[gb2], %[bbase]\n"
-      "  global_load_dwordx4 v[44:47], %[gb3], %[bbase]\n"
-      ".endm\n"
-      // Store the prefetched k-tile into the LDS buffer the write addresses name.
-      ".macro VK_ST\n"
-      "  .irp e, 0,1\n"
-      "  .irp q, 0,1,2,3\n"
-      "  ds_write_b32 %[wr_a], v[112+4*\\e+\\q] offset:(\\q*528+\\e*256)\n"
-      "  .endr\n"
-      "  .endr\n"
-      "  .irp e, 0,1,2,3\n"
-      "  ds_write_b128 %[wr_b], v[32+4*\\e:35+4*\\e] offset:(\\e*4096)\n"
-      "  .endr\n"
+      // k-tile loads at the current global offsets into the LDS buffer at a_dst / b_dst
+      ".macro VK_DMA\n"
+      "  s_mov_b32 m0, %[a_dst]\n"
+      "  s_nop 0\n"
+      "  global_load_lds_dwordx4 %[ga0], %[abase]\n"
+      "  s_add_u32 m0, %[a_dst], 1024\n"
+      "  s_nop 0\n"
+      "  global_load_lds_dwordx4 %[ga1], %[abase]\n"
+      "  s_mov_b32 m0, %[b_dst]\n"
+      "  s_nop 0\n"
+      "  global_load_lds_dwordx4 %[gb0], %[bbase]\n"
+      "  s_add_u32 m0, %[b_dst], 4096\n"
+      "  s_nop 0\n"
+      "  global_load_lds_dwordx4 %[gb1], %[bbase]\n"
+      "  s_add_u32 m0, %[b_dst], 8192\n"
+      "  s_nop 0\n"
+      "  global_load_lds_dwordx4 %[gb2], %[bbase]\n"
+      "  s_add_u32 m0, %[b_dst], 12288\n"
+      "  s_nop 0\n"
+      "  global_load_lds_dwordx4 %[gb3], %[bbase]\n"
       ".endm\n"
       ".macro VK_ADV\n"
       "  v_add_u32 %[ga0], %[astep], %[ga0]\n"
@@ -286,62 +283,72 @@ __global__ __launch_bounds__(256) void f32_valu_asm_kernel(const float* __restri
       "  v_add_u32 %[gb2], %[bstep], %[gb2]\n"
       "  v_add_u32 %[gb3], %[bstep], %[gb3]\n"
       ".endm\n"
-      // accumulators = 0
+      // A rows of k-chunk at address ADDR into a-buffer AQ (8 x 16 B)
+      ".macro VK_RDA AQ, ADDR\n"
+      "  .irp i, 0,1,2,3\n"
+      "  ds_read_b128 v[\\AQ+4*\\i:\\AQ+4*\\i+3], \\ADDR offset:(\\i*64)\n"
+      "  ds_read_b128 v[\\AQ+16+4*\\i:\\AQ+16+4*\\i+3], \\ADDR offset:(4096+\\i*64)\n"
+      "  .endr\n"
+      ".endm\n"
+      ".macro VK_RDB KK, BB\n"
+      "  .irp g, 0,1,2,3\n"
+      "  ds_read_b128 v[\\BB+4*\\g:\\BB+4*\\g+3], %[rd_b] offset:(\\KK*1024+\\g*256)\n"
+      "  .endr\n"
+      ".endm\n"
+      // 128 FMAs of k-step KK (a-buffer AQ, b-buffer BB); a[i] of row i in
+      // v[AQ + 4 i + KK % 4] for i < 4 and v[AQ + 16 + 4 (i - 4) + KK % 4]
+      ".macro VK_FMA AQ, KK, BB\n"
+      "  .irp i, 0,1,2,3,4,5,6,7\n"
+      "  .irp j, 0,1,2,3,4,5,6,7,8,9,10,11,12,13,14,15\n"
+      "  v_fmac_f32 v[128+16*\\i+((\\j+1)&15)], v[\\AQ+4*\\i+(\\KK&3)], v[\\BB+\\j]\n"
+      "  .endr\n"
+      "  .endr\n"
+      ".endm\n"
       "  .irp r, 0,16,32,48,64,80,96,112\n"
       "  .irp c, 0,1,2,3,4,5,6,7,8,9,10,11,12,13,14,15\n"
       "  v_mov_b32 v[128+\\r+\\c], 0\n"
       "  .endr\n"
       "  .endr\n"
-      // prologue: k-tile 0 into LDS buffer 0, then the write addresses move
-      // to buffer 1 and k-step 0 is read
-      "  VK_GLD\n"
+      // prologue: k-tile 0 into buffer 0
+      "  VK_DMA\n"
       "  VK_ADV\n"
       "  s_waitcnt vmcnt(0)\n"
-      "  VK_ST\n"
-      "  v_sub_u32 %[wr_a], %[sum_wa], %[wr_a]\n"
-      "  v_sub_u32 %[wr_b], %[sum_wb], %[wr_b]\n"
-      "  s_waitcnt lgkmcnt(0)\n"
       "  s_barrier\n"
-      "  VK_RD 0, 96, 64\n"
-      "L_vk_tile_%=:\n"
+      "L_vkd_tile_%=:\n"
+      // the next k-tile into the other buffer (freed by the barrier just passed)
+      "  s_sub_u32 %[a_dst], %[sa_dst], %[a_dst]\n"
+      "  s_sub_u32 %[b_dst], %[sb_dst], %[b_dst]\n"
       "  s_cmp_gt_u32 %[nk], 1\n"
-      "  s_cbranch_scc0 L_vk_noload_%=\n"
-      "  VK_GLD\n"
+      "  s_cbranch_scc0 L_vkd_noload_%=\n"
+      "  VK_DMA\n"
       "  VK_ADV\n"
-      "L_vk_noload_%=:\n"
+      "L_vkd_noload_%=:\n"
+      "  VK_RDA 32, %[rd_a]\n"
+      "  VK_RDB 0, 64\n"
       "  s_waitcnt lgkmcnt(0)\n"
-      // k-steps 0..13 in pairs, then 14 and 15
-      "  .irp kk, 0,2,4,6,8,10,12\n"
-      "  VK_RD (\\kk+1), 104, 80\n"
-      "  VK_FMA 96, 64\n"
-      "  s_waitcnt lgkmcnt(0)\n"
-      "  VK_RD (\\kk+2), 96, 64\n"
-      "  VK_FMA 104, 80\n"
+      // k-steps 0..14: the reads of k-step kk + 1 (and of the next A group)
+      // go out ahead of k-step kk's FMAs
+      "  .irp kk, 0,1,2,3,4,5,6,7,8,9,10,11,12,13,14\n"
+      "  VK_RDB (\\kk+1), (64+16*((\\kk+1)&1))\n"
+      "  .if ((\\kk+1)&3) == 0\n"
+      "  v_xor_b32 %[tmp], 16*((\\kk+1)>>2), %[rd_a]\n"
+      "  VK_RDA (32+64*(((\\kk+1)>>2)&1)), %[tmp]\n"
+      "  .endif\n"
+      "  VK_FMA (32+64*((\\kk>>2)&1)), \\kk, (64+16*(\\kk&1))\n"
       "  s_waitcnt lgkmcnt(0)\n"
       "  .endr\n"
-      "  VK_RD 15, 104, 80\n"
-      "  VK_FMA 96, 64\n"
-      "  s_waitcnt lgkmcnt(0)\n"
-      "  VK_FMA 104, 80\n"
+      "  VK_FMA 96, 15, 80\n"
       "  s_cmp_gt_u32 %[nk], 1\n"
-      "  s_cbranch_scc0 L_vk_done_%=\n"
-      // next k-tile: store it into the other LDS buffer, barrier, switch the
-      // read and write buffers, read its k-step 0
+      "  s_cbranch_scc0 L_vkd_done_%=\n"
+      // this wave's loads of the next k-tile have landed; after the barrier
+      // every wave's have, and every wave is done reading this buffer
       "  s_waitcnt vmcnt(0)\n"
-      "  VK_ST\n"
-      "  v_sub_u32 %[wr_a], %[sum_wa], %[wr_a]\n"
-      "  v_sub_u32 %[wr_b], %[sum_wb], %[wr_b]\n"
+      "  s_barrier\n"
       "  v_sub_u32 %[rd_a], %[sum_a], %[rd_a]\n"
       "  v_sub_u32 %[rd_b], %[sum_b], %[rd_b]\n"
-      "  s_waitcnt lgkmcnt(0)\n"
-      "  s_barrier\n"
-      "  s_nop 1\n"
-      "  VK_RD 0, 96, 64\n"
       "  s_sub_u32 %[nk], %[nk], 1\n"
-      "  s_branch L_vk_tile_%=\n"
-      "L_vk_done_%=:\n"
-      // C: each row's 16 accumulators are gathered in column order into
-      // v[48:127] (4 rows at a time) and stored as 4 x 16 bytes per row
+      "  s_branch L_vkd_tile_%=\n"
+      "L_vkd_done_%=:\n"
       "  .irp half, 0,1\n"
       "  .irp i, 0,1,2,3\n"
       "  .irp j, 0,1,2,3,4,5,6,7,8,9,10,11,12,13,14,15\n"
@@ -366,18 +373,19 @@ __global__ __launch_bounds__(256) void f32_valu_asm_kernel(const float* __restri
       "  .endr\n"
       "  s_waitcnt vmcnt(0)\n"
       "  .endr\n"
-      ".purgem VK_RD\n"
-      ".purgem VK_FMA\n"
-      ".purgem VK_GLD\n"
-      ".purgem VK_ST\n"
+      ".purgem VK_DMA\n"
       ".purgem VK_ADV\n"
+      ".purgem VK_RDA\n"
+      ".purgem VK_RDB\n"
+      ".purgem VK_FMA\n"
       : [ga0] "+v"(ga0), [ga1] "+v"(ga1), [gb0] "+v"(gb0), [gb1] "+v"(gb1), [gb2] "+v"(gb2), [gb3] "+v"(gb3),
-        [rd_a] "+v"(rd_a), [rd_b] "+v"(rd_b), [wr_a] "+v"(wr_a), [wr_b] "+v"(wr_b), [c_lo] "+v"(c_lo),
-        [c_hi] "+v"(c_hi), [nk] "+s"(nk)
+        [rd_a] "+v"(rd_a), [rd_b] "+v"(rd_b), [c_lo] "+v"(c_lo), [c_hi] "+v"(c_hi), [tmp] "=&v"(tmp),
+        [nk] "+s"(nk), [a_dst] "+s"(a_dst), [b_dst] "+s"(b_dst)
       : [abase] "s"(abase), [bbase] "s"(bbase), [cbase] "s"(cbase), [astep] "s"(astep), [bstep] "s"(bstep),
-        [crow] "s"(crow), [sum_a] "v"(sum_a), [sum_b] "v"(sum_b), [sum_wa] "v"(sum_wa), [sum_wb] "v"(sum_wb)
-      : "memory", VK_CLOBBER_V32_V255);
+        [crow] "s"(crow), [sum_a] "v"(sum_a), [sum_b] "v"(sum_b), [sa_dst] "s"(sa_dst), [sb_dst] "s"(sb_dst)
+      : "memory", "m0", VK_CLOBBER_V32_V255);
 }
+#pragma clang diagnostic pop
 
 hipError_t launch_f32(const GemmArgs& a) {
   dim3 grid((unsigned)((a.n + kTN - 1) / kTN), (unsigned)((a.m + kTM - 1) / kTM));

@@ -164,11 +164,13 @@ __device__ __forceinline__ void lds_barrier() {
 // asm so the compiler does not track it: it would otherwise treat every later
 // LDS read as aliasing the pending load and wait for all of them (vmcnt(0)),
 // which would drain a prefetch ring.  Completion is awaited explicitly with
-// wait_vmcnt().  Nothing else in these kernels uses M0.
+// wait_vmcnt().  Nothing else in these kernels uses M0.  An SALU write of M0
+// followed by an LDS-DMA load needs one wait state on the GFX9 family (the
+// s_nop 0); the compiler inserts it for its own code, not inside inline asm.
 #pragma clang diagnostic push
 #pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t lds_dst) {
-  asm volatile("s_mov_b32 m0, %0\n\tglobal_load_lds_dwordx4 %1, %2"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %1, %2"
                :
                : "s"(lds_dst), "v"(voff), "s"(gbase)
                : "m0");
@@ -179,7 +181,7 @@ __device__ __forceinline__ void dma16(const void* gbase, uint32_t voff, uint32_t
 // MI355X), which is how a lane outside a matrix is masked.
 __device__ __forceinline__ void dma16_buf(__amdgpu_buffer_rsrc_t rsrc, uint32_t voff, uint32_t soff,
                                           uint32_t lds_dst) {
-  asm volatile("s_mov_b32 m0, %0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
+  asm volatile("s_mov_b32 m0, %0\n\ts_nop 0\n\tbuffer_load_dwordx4 %1, %2, %3 offen lds"
                :
                : "s"(lds_dst), "v"(voff), "s"(rsrc), "s"(soff)
                : "m0");
