@@ -13,8 +13,10 @@ F16_CASES = [
     ((1, 256, 64), 8),           # one row: the skinny split-K kernel
     ((200, 1024, 2048), 8),      # 2 x 2 waves
     ((16, 8224, 256), 8),        # n % 128 != 0: the last column block cut short
-    ((512, 512, 512), 7),        # on the 256 x 256 x 64 grid
-    ((2048, 2048, 4096), 9),     # 64 tiles: split tail
+    ((4096, 4096, 256), 7),      # one full wave of 256 x 256 tiles
+    ((512, 512, 512), 11),       # 16 tiles of 128 x 128 where 256 x 256 gives 4 (and no split)
+    ((2048, 2048, 4096), 11),    # 256 tiles of 128 x 128: one wave
+    ((1024, 1024, 8192), 9),     # 64 tiles of 128 x 128: the split tail of 16 large tiles
     ((300, 264, 72), 10),        # off the grid
     ((1000, 1000, 4000), 10),    # off the grid, split tail
     ((512, 512, 544), 10),       # k % 64 != 0

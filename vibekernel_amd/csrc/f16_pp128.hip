@@ -1,0 +1,340 @@
+// f16_pp128.hip -- fp16 GEMM, version 11: version 7's ping-pong on 128x128
+// tiles with 128-deep k-tiles, for grids that 256x256 tiles leave part empty.
+//
+// At 4096^3 a 256x256 tile per CU is the cheapest way to feed the matrix
+// cores (f16_pingpong.hip).  A GEMM with few such tiles -- 1024 x 4096 x
+// 4096 has 64 on 256 CUs -- must otherwise split K (version 9), and each
+// split tile's pieces meet through fp32 partials that cost as much as the
+// k-loop (measured: ~24 us of k-loop, 47.6 us per launch).  Here four times
+// as many tiles fill the CUs instead, and no partial leaves a CU.  The price
+// is twice the L2->LDS and LDS-read bytes per FLOP of the 256x256 tile.
+//
+// Same design as version 7 scaled down, with 128-deep k-tiles so that a
+// phase still holds 512 matrix-core cycles:
+//  * 512 threads = 8 waves: P = waves 0..3 own tile rows 0..63, Q = waves
+//    4..7 rows 64..127; wave g of a group owns columns 32g..32g+31, a 64x32
+//    block = 4x2 MFMA blocks of 16x16 (32 fp32 accumulators per lane);
+//  * per k-tile each group runs a memory phase (this wave's 16 A-fragment
+//    reads and 16 transposed B reads of the k-tile) and a compute phase (32
+//    v_mfma_f32_16x16x32_f16, each accumulator's 4 k-steps back to back, and
+//    this wave's 8 direct-to-LDS loads of k-tile t+2, one after each
+//    accumulator's chain); Q runs one phase behind P;
+//  * LDS ring (160 KB), the slot sizes of version 7's:
+//      A-top  rows  0..63 of the A k-tile (64 x 128 k), read by P  2 x 16 KB
+//      A-bot  rows 64..127,                               read by Q  2 x 16 KB
+//      B      128 k x 128 columns,                        read by both 3 x 32 KB
+//    Q loads A-top(t+2) and A-bot(t+2) into slot t % 2, P loads B(t+2) into
+//    slot (t+2) % 3, with version 7's waits (vmcnt 4 and 8);
+//  * A rows are 256 B = 16 chunks of 16 B, chunk ^ (row % 16): the 16 rows of
+//    a fragment read sit in 16 distinct chunks; B k-rows are 256 B too,
+//    chunk ^ 2 (k % 4) ^ 8 bit3(k) (the skinny kernel's transpose-read
+//    swizzle for 16-chunk rows);
+//  * the epilogue stages each wave's 64x32 block of C through LDS (8-byte
+//    units XOR (row / 4) % 8 for fp16, 16-byte chunks XOR (row / 2) % 8 for
+//    fp32) and stores 16-byte pieces of full row segments.
+// M, N and K multiples of 128.
+#include "vk_device.hpp"
+#include "vk_internal.hpp"
+#include "vk_tile.hpp"
+
+#include <atomic>
+
+namespace vk {
+namespace {
+namespace pp128 {
+
+constexpr int kBM = 128, kBN = 128, kBK = 128;
+constexpr int kThreads = 512;
+constexpr int kRowBytes = kBK * 2;                // 256: an A row of a k-tile
+constexpr int kHalfBytes = 64 * kRowBytes;        // 16 KB: one A half-tile
+constexpr int kBRowBytes = kBN * 2;               // 256: a B k-row of a tile
+constexpr int kBBytes = kBK * kBRowBytes;         // 32 KB
+constexpr int kATop = 0;                          // 2 slots
+constexpr int kABot = 2 * kHalfBytes;             // 2 slots
+constexpr int kBOff = 4 * kHalfBytes;             // 3 slots
+constexpr int kBSlots = 3;
+constexpr int kLdsBytes = kBOff + kBSlots * kBBytes;  // 160 KB
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+static_assert(kLdsBytes >= 8 * 64 * 32 * 4, "fp32 epilogue staging: 8 KB per wave");
+
+__host__ __device__ constexpr int swz_a(int row) { return row & 15; }
+__host__ __device__ constexpr int swz_b(int krow) { return (2 * (krow & 3)) ^ (((krow >> 3) & 1) << 3); }
+
+// Store of a wave's 64x32 block of C.  Block (i, j), register r, lane l
+// holds C[16 i + l % 16][16 j + 4 (l / 16) + r].
+template <typename OutT>
+struct Epi;
+
+// fp16: rows of 64 B = 8 units of 8 B (4 halves); unit u of row r at
+// u ^ (r / 4) % 8.  A write instruction's 16 lanes of one unit column name
+// 16 consecutive rows: rows 4 apart share banks, and the XOR moves them to
+// distinct units.  A read takes units 2c, 2c+1 (16 B) at the unit pair
+// c ^ (r / 8) % 4, halves swapped when (r / 4) is odd.
+template <>
+struct Epi<half_t> {
+  static constexpr int kRegion = 64 * 64;
+  static __device__ __forceinline__ void stage(uint32_t wbase, int lane, int i, int j, const float4v& v) {
+    const int row = 16 * i + (lane & 15), unit = 4 * j + (lane >> 4);
+    half4 h = {(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
+    lds_write8(wbase + row * 64 + 8 * (unit ^ ((row >> 2) & 7)), h);
+  }
+  static __device__ __forceinline__ void store(uint32_t wbase, half_t* Cw, int N, int lane) {
+    const int rsub = lane >> 2, ch = lane & 3;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int row = 16 * q + rsub;
+      const int f = (row >> 2) & 7;
+      const uint4v v = lds_read16(wbase + row * 64 + 16 * (ch ^ (f >> 1)));
+      const bool odd = f & 1;
+      const uint4v o = {odd ? v[2] : v[0], odd ? v[3] : v[1], odd ? v[0] : v[2], odd ? v[1] : v[3]};
+      *reinterpret_cast<uint4v*>(Cw + (size_t)row * N + ch * 8) = o;
+    }
+  }
+};
+
+// fp32: rows of 128 B = 8 chunks of 16 B (4 floats); chunk u of row r at
+// u ^ (r / 2) % 8.
+template <>
+struct Epi<float> {
+  static constexpr int kRegion = 64 * 128;
+  static __device__ __forceinline__ void stage(uint32_t wbase, int lane, int i, int j, const float4v& v) {
+    const int row = 16 * i + (lane & 15), chunk = 4 * j + (lane >> 4);
+    lds_write16(wbase + row * 128 + 16 * (chunk ^ ((row >> 1) & 7)), v);
+  }
+  static __device__ __forceinline__ void store(uint32_t wbase, float* Cw, int N, int lane) {
+    const int rsub = lane >> 3, ch = lane & 7;
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const int row = 8 * q + rsub;
+      const uint4v v = lds_read16(wbase + row * 128 + 16 * (ch ^ ((row >> 1) & 7)));
+      *reinterpret_cast<uint4v*>(Cw + (size_t)row * N + ch * 4) = v;
+    }
+  }
+};
+
+template <typename OutT>
+__global__ __launch_bounds__(kThreads) void f16_pp128_kernel(const half_t* __restrict__ A,
+                                                             const half_t* __restrict__ B,
+                                                             OutT* __restrict__ C, int M, int N, int K) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;  // 0 = P, 1 = Q; waves w and w+4 share a SIMD
+  const int gw = wave & 3;
+  int tm, tn;
+  tile_of(blockIdx.x, M / kBM, N / kBN, tm, tn);
+  const int m0 = tm * kBM, n0 = tn * kBN;
+  const int nk = K / kBK;
+  const uint32_t lds_base = lds_addr32(lds);
+
+  // ---- direct-to-LDS duty: instruction d = 4h + i (8 per wave per k-tile) ----
+  // Q, A: rows gw*16 + 4i + l/16 of the A-top (h = 0) or A-bot (h = 1) half
+  //   (4 rows of 256 B per 1 KB instruction; lane l lands at chunk position
+  //   l % 16, which holds chunk (l % 16) ^ swz_a(row)), at half offset
+  //   (gw*16 + 4i) * 256.
+  // P, B: k-rows gw*32 + 16h + 4i + l/16, landing at their own row offset;
+  //   h moves 16 k-rows (bit 4), which the B swizzle ignores, so voff[i]
+  //   serves both h.
+  uint32_t voff[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    if (grp) {
+      const int row = gw * 16 + 4 * i + (lane >> 4);
+      const int c = (lane & 15) ^ swz_a(row);
+      voff[i] = (uint32_t)(((size_t)row * K + c * 8) * 2);
+    } else {
+      const int krow = gw * 32 + 4 * i + (lane >> 4);
+      const int c = (lane & 15) ^ swz_b(krow);
+      voff[i] = (uint32_t)(((size_t)krow * N + c * 8) * 2);
+    }
+  }
+  const char* g_base = grp ? reinterpret_cast<const char*>(A) + (size_t)m0 * K * 2
+                           : reinterpret_cast<const char*>(B) + (size_t)n0 * 2;
+  const size_t g_kt = grp ? (size_t)kBK * 2 : (size_t)kBK * N * 2;   // per k-tile
+  const size_t g_h = grp ? (size_t)64 * K * 2 : (size_t)16 * N * 2;  // per h
+  const uint32_t l_base = lds_base + (grp ? (uint32_t)kATop + gw * 16 * kRowBytes : (uint32_t)kBOff + gw * 32 * kBRowBytes);
+  const uint32_t l_slot = grp ? (uint32_t)kHalfBytes : (uint32_t)kBBytes;  // per slot
+  const uint32_t l_h = grp ? (uint32_t)(kABot - kATop) : 16u * kBRowBytes;  // per h
+
+  // Scalar operands of the 8 loads of one k-tile, computed in the memory
+  // phase so that the compute phase issues each load as M0, its wait state
+  // and the load between two MFMAs.
+  struct DmaOps {
+    const char* g[2];  // global base of half h
+    uint32_t l[8];     // LDS destination of load d
+  };
+  auto dma_ops = [&](int kt, int slot) {
+    DmaOps o;
+    const uint32_t ls = l_base + slot * l_slot;
+#pragma unroll
+    for (int h = 0; h < 2; h++) {
+      o.g[h] = g_base + (size_t)kt * g_kt + h * g_h;
+#pragma unroll
+      for (int i = 0; i < 4; i++) o.l[4 * h + i] = ls + h * l_h + i * 1024;
+    }
+    return o;
+  };
+  auto pin_ops = [&](const DmaOps& o) {
+    asm volatile("" ::"s"(o.g[0]), "s"(o.g[1]));
+    asm volatile("" ::"s"(o.l[0]), "s"(o.l[1]), "s"(o.l[2]), "s"(o.l[3]), "s"(o.l[4]), "s"(o.l[5]), "s"(o.l[6]),
+                 "s"(o.l[7]));
+  };
+  auto dma_with = [&](int d, const DmaOps& o) { dma16(o.g[d >> 2], voff[d & 3], o.l[d]); };
+  auto dma = [&](int d, int kt, int slot) { dma_with(d, dma_ops(kt, slot)); };
+
+  // ---- fragment addresses ----
+  // A block i, k-step s: half-row 16i + l%16, chunk 4s + l/16 (the row's
+  // swizzle is that of l%16 for every i).
+  const int arow = lane & 15;
+  const uint32_t a_half = grp ? kABot : kATop;
+  uint32_t aoff[4];
+#pragma unroll
+  for (int s = 0; s < 4; s++) aoff[s] = a_half + arow * kRowBytes + 16 * ((4 * s + (lane >> 4)) ^ swz_a(arow));
+  // B block j, k-step s, half h: lane 16g + 4jj + q names k-row
+  // 32s + 8g + 4h + jj, columns 32 gw + 16j + 4q .. +3; the transpose read
+  // hands lane 16g + c the 4 k of column 16j + c.
+  const int g = lane >> 4, jj = (lane >> 2) & 3, q = lane & 3;
+  const int krow0 = 8 * g + jj;  // plus 32s + 4h: bits 0, 1, 3 unchanged
+  uint32_t boff[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int c = gw * 4 + 2 * j + (q >> 1);
+    boff[j] = kBOff + krow0 * kBRowBytes + 16 * (c ^ swz_b(krow0)) + 8 * (q & 1);
+  }
+
+  float4v acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+  half8 fa[4][4], fb[4][2];  // [k-step][block]
+  auto read_frags = [&](int aslot, int bslot) {
+    const uint32_t sa = lds_base + aslot * kHalfBytes;
+    const uint32_t sb = lds_base + bslot * kBBytes;
+    uint32_t va[4], vb[2];
+#pragma unroll
+    for (int s = 0; s < 4; s++) va[s] = sa + aoff[s];
+#pragma unroll
+    for (int j = 0; j < 2; j++) vb[j] = sb + boff[j];
+    static_for<4>([&](auto sc) {
+      constexpr int s = decltype(sc)::value;
+      static_for<4>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        fa[s][i] = lds_read_h8_off<i * 16 * kRowBytes>(va[s]);
+      });
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+        const half4 lo = lds_read_tr16_off<s * 32 * kBRowBytes>(vb[j]);
+        const half4 hi = lds_read_tr16_off<s * 32 * kBRowBytes + 4 * kBRowBytes>(vb[j]);
+        fb[s][j] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+    });
+  };
+  // 32 MFMAs, each accumulator's 4 k-steps back to back (k ascending), and
+  // the 8 loads described by `o`, one after each accumulator.
+  auto compute_and_load = [&](const DmaOps& o) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+#pragma unroll
+      for (int j = 0; j < 2; j++) {
+#pragma unroll
+        for (int s = 0; s < 4; s++) {
+          acc[i][j] = mfma16x16x32(fb[s][j], fa[s][i], acc[i][j]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        dma_with(2 * i + j, o);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+
+  // Prologue and loop: version 7's phases and waits.
+  const int kt1 = min(1, nk - 1);
+#pragma unroll
+  for (int d = 0; d < 8; d++) dma(d, 0, 0);
+#pragma unroll
+  for (int d = 0; d < 8; d++) dma(d, kt1, 1);
+  if (grp)
+    wait_vmcnt<12>();
+  else
+    wait_vmcnt<8>();
+  lds_barrier();
+  if (grp) {
+    wait_vmcnt<8>();
+    lds_barrier();
+  }
+
+  for (int t = 0; t < nk; t++) {
+    const int aslot = t & 1;
+    const int bslot = t % kBSlots;
+    const int kt2 = min(t + 2, nk - 1);
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(aslot, bslot);
+    __builtin_amdgcn_sched_barrier(0);  // the reads go out first
+    const DmaOps ops = dma_ops(kt2, grp ? aslot : (t + 2) % kBSlots);
+    pin_ops(ops);
+    if (grp) wait_vmcnt<4>();  // Q: A-top(t+1) landed before barrier 2t+2
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    compute_and_load(ops);
+    wait_vmcnt<8>();  // P: B(t+1); Q: A-top(t+1), A-bot(t+1)
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (!grp) lds_barrier();
+  wait_vmcnt<0>();
+  lds_barrier();
+
+  // ---- epilogue: the ring is idle; each wave stages its block in its own region ----
+  const uint32_t wstage = lds_base + wave * Epi<OutT>::kRegion;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) Epi<OutT>::stage(wstage, lane, i, j, acc[i][j]);
+  wait_lgkmcnt0();  // a wave reads back only its own region
+  Epi<OutT>::store(wstage, C + (size_t)(m0 + grp * 64) * N + n0 + gw * 32, N, lane);
+}
+
+template <typename OutT>
+hipError_t launch_t(const GemmArgs& a) {
+  static std::atomic<uint64_t> attr_done{0};
+  auto kfn = f16_pp128_kernel<OutT>;
+  hipError_t e = ensure_lds_attr(kfn, kLdsBytes, a.device, attr_done);
+  if (e != hipSuccess) return e;
+  const int tiles = (int)((a.m / kBM) * (a.n / kBN));
+  hipLaunchKernelGGL(kfn, dim3(tiles), dim3(kThreads), kLdsBytes, a.stream, static_cast<const half_t*>(a.A),
+                     static_cast<const half_t*>(a.B), static_cast<OutT*>(a.C), (int)a.m, (int)a.n, (int)a.k);
+  return hipGetLastError();
+}
+
+hipError_t launch(const GemmArgs& a) {
+  return a.out_dtype == VK_DTYPE_F16 ? launch_t<half_t>(a) : launch_t<float>(a);
+}
+
+// 32-bit lane offsets (64 rows of A, 128 k-rows of B past the scalar base)
+// and the 1-D grid.
+bool shape_ok(size_t m, size_t n, size_t k) {
+  return (size_t)kBM * k * 2 < (1ull << 31) && (size_t)kBK * n * 2 < (1ull << 31) &&
+         (m / kBM) * (n / kBN) < (1ull << 31);
+}
+
+}  // namespace pp128
+}  // namespace
+
+void register_f16_pp128() {
+  KernelEntry e{};
+  e.version = 11;
+  e.in_dtype = VK_DTYPE_F16;
+  e.name = "f16_v11_pp128_bk128";
+  e.caps = make_caps(11, VK_DTYPE_F16, kOutF16 | kOutF32, pp128::kBM, pp128::kBN, pp128::kBK, 16, pp128::kBM,
+                     pp128::kBN, pp128::kBK, pp128::kThreads, pp128::kLdsBytes, 0, 0);
+  e.launch = pp128::launch;
+  e.workspace = nullptr;
+  e.shape_ok = pp128::shape_ok;
+  register_kernel(e);
+}
+
+}  // namespace vk

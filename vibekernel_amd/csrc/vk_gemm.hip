@@ -51,6 +51,7 @@ void init_registry() {
     register_f16_dma();
     register_f16_skinny();
     register_f16_pingpong();
+    register_f16_pp128();
     register_f16_skinny_sk();
     register_f32_valu();
     register_f32_mfma();

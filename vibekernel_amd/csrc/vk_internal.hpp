@@ -57,6 +57,7 @@ void register_f16_simple();
 void register_f16_dma();
 void register_f16_skinny();
 void register_f16_pingpong();
+void register_f16_pp128();
 void register_f16_skinny_sk();
 void register_f32_valu();
 void register_f32_mfma();

@@ -97,24 +97,48 @@ def query(version: int, dtype: str = "f16"):
     return _abi.query(version, DTYPE_F16 if dtype == "f16" else DTYPE_F32)
 
 
+def _num_cus() -> int:
+    """Compute units of the current device (256 on MI355X, assumed when no
+    device is visible)."""
+    try:
+        torch = _torch()
+        if torch.cuda.is_available():
+            return torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
+    except Exception:
+        pass
+    return 256
+
+
 def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = None) -> int:
     """The fastest version that accepts this shape (checked with vk_gemm_check
     on 4 KiB-aligned placeholder addresses; nothing is launched): for fp16
-    the skinny kernels when M <= 256 (64 for version 4), then the 256x256
-    kernels (fastest first; version 10 takes shapes off the 256 x 256 x 64
-    grid whose N and K are multiples of 8), then the any-shape kernel.  The
-    split-tail version 9 comes first among the 256x256 kernels only where its
-    schedule splits tiles on this device (it then needs a workspace);
-    elsewhere it would run version 7's whole tiles.  The reference picks
-    versions at build time only (CMakeLists.txt MATMUL_VERSION); this is a
-    convenience of the front end."""
+    the skinny kernels when M <= 256 (64 for version 4), then the 128 x 128
+    tiles of version 11 where they make one wave of the compute units and
+    either fill more than a quarter of them or the split-tail plan splits
+    nothing (measured on MI355X: 1024 x 4096 x 4096 33.6 us against 46.2 for
+    version 9 and 64.5 for version 7; 1024 x 1024 x 8192, 64 such tiles,
+    47.3 against version 9's 43.9), then the 256x256 kernels (fastest first;
+    version 10 takes shapes off the 256 x 256 x 64 grid whose N and K are
+    multiples of 8), then the any-shape kernel.  The split-tail version 9
+    comes first among the 256x256 kernels only where its schedule splits
+    tiles on this device (it then needs a workspace); elsewhere it would run
+    version 7's whole tiles.  The reference picks versions at build time only
+    (CMakeLists.txt MATMUL_VERSION); this is a convenience of the front end."""
     in_dt = DTYPE_F16 if dtype == "f16" else DTYPE_F32
     out_dt = DTYPE_F16 if (out or dtype) == "f16" else DTYPE_F32
-    order = [8, 4, 9, 7, 10, 6, 5, 3, 2, 1] if in_dt == DTYPE_F16 else [2, 3, 1]
+    order = [8, 4, 11, 9, 7, 10, 6, 5, 3, 2, 1] if in_dt == DTYPE_F16 else [2, 3, 1]
     avail = set(_abi.versions(in_dt))
+    cus = None
     for v in order:
+        if v not in avail:
+            continue
         if v == 9 and _abi.workspace_bytes(v, in_dt, m, n, k) == 0:
             continue
-        if v in avail and _abi.check(v, in_dt, out_dt, m, n, k, 4096, 4096, 4096) == _abi.VK_OK:
+        if v == 11:
+            cus = cus or _num_cus()
+            tiles = (m // 128) * (n // 128)
+            splits = 9 in avail and _abi.workspace_bytes(9, in_dt, m, n, k) > 0
+            if not (tiles <= cus and (4 * tiles > cus or not splits)):
+                continue
+        if _abi.check(v, in_dt, out_dt, m, n, k, 4096, 4096, 4096) == _abi.VK_OK:
             return v
-    raise VkError(-3, f"no {dtype} version accepts m={m}, n={n}, k={k}")
