@@ -30,8 +30,8 @@
 //    chunk ^ 2 (k % 4) ^ 8 bit3(k) (the skinny kernel's transpose-read
 //    swizzle for 16-chunk rows);
 //  * the epilogue stages each wave's 64x32 block of C through LDS (8-byte
-//    units XOR (row / 4) % 8 for fp16, 16-byte chunks XOR (row / 2) % 8 for
-//    fp32) and stores 16-byte pieces of full row segments.
+//    units XOR 2 ((row / 4) % 4) for fp16, 16-byte chunks XOR (row / 2) % 8
+//    for fp32) and stores 16-byte pieces of full row segments.
 // M, N and K multiples of 128.
 #include "vk_device.hpp"
 #include "vk_internal.hpp"
@@ -66,28 +66,27 @@ template <typename OutT>
 struct Epi;
 
 // fp16: rows of 64 B = 8 units of 8 B (4 halves); unit u of row r at
-// u ^ (r / 4) % 8.  A write instruction's 16 lanes of one unit column name
-// 16 consecutive rows: rows 4 apart share banks, and the XOR moves them to
-// distinct units.  A read takes units 2c, 2c+1 (16 B) at the unit pair
-// c ^ (r / 8) % 4, halves swapped when (r / 4) is odd.
+// u ^ 2 ((r / 4) % 4).  Rows 4 apart share banks; a write instruction's
+// 32-lane half names 16 rows x 2 unit columns, and the XOR (which keeps
+// unit bit 0) puts them on 8 distinct units per bank class: two passes per
+// instruction, the least its 512 bytes take.  A read takes units 2c, 2c+1
+// (16 B) at the unit pair c ^ (r / 4) % 4.
 template <>
 struct Epi<half_t> {
   static constexpr int kRegion = 64 * 64;
+  static __device__ __forceinline__ int swz(int row) { return ((row >> 2) & 3) << 1; }
   static __device__ __forceinline__ void stage(uint32_t wbase, int lane, int i, int j, const float4v& v) {
     const int row = 16 * i + (lane & 15), unit = 4 * j + (lane >> 4);
     half4 h = {(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
-    lds_write8(wbase + row * 64 + 8 * (unit ^ ((row >> 2) & 7)), h);
+    lds_write8(wbase + row * 64 + 8 * (unit ^ swz(row)), h);
   }
   static __device__ __forceinline__ void store(uint32_t wbase, half_t* Cw, int N, int lane) {
     const int rsub = lane >> 2, ch = lane & 3;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const int row = 16 * q + rsub;
-      const int f = (row >> 2) & 7;
-      const uint4v v = lds_read16(wbase + row * 64 + 16 * (ch ^ (f >> 1)));
-      const bool odd = f & 1;
-      const uint4v o = {odd ? v[2] : v[0], odd ? v[3] : v[1], odd ? v[0] : v[2], odd ? v[1] : v[3]};
-      *reinterpret_cast<uint4v*>(Cw + (size_t)row * N + ch * 8) = o;
+      const uint4v v = lds_read16(wbase + row * 64 + 16 * (ch ^ (swz(row) >> 1)));
+      *reinterpret_cast<uint4v*>(Cw + (size_t)row * N + ch * 8) = v;
     }
   }
 };
