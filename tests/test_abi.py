@@ -140,7 +140,7 @@ def test_pick_version_follows_shape():
     assert vk.pick_version(144, 8192, 8192) == 8  # 2 x 2 waves up to 256 rows
     assert vk.pick_version(1, 8192, 8192) == 8    # one row: the same kernel, rows past M read as zeros
     assert vk.pick_version(256, 8192, 8192) == 8
-    assert vk.pick_version(300, 8192, 8192) == 10  # beyond 256 rows: v7 with edges
+    assert vk.pick_version(300, 8192, 8192) == 11  # beyond 256 rows, off the grid: 192 tiles of 128 x 128
     assert vk.pick_version(4096, 4096, 4096) == 7  # 256 tiles: one full wave
     assert vk.pick_version(4096, 4096, 4096, "f16", "f32") == 7
     assert vk.pick_version(4096, 11008, 4096) == 7  # 688 tiles = 2.69 waves: tail left whole
@@ -151,7 +151,8 @@ def test_pick_version_follows_shape():
     assert vk.pick_version(4096, 4096, 4128) == 10  # k % 64 != 0: v7 with a masked last k-tile
     assert vk.pick_version(100, 300, 70) == 1
     assert vk.pick_version(4000, 4000, 4000) == 10  # off the 256 x 256 x 64 grid: v7 with edges
-    assert vk.pick_version(1000, 1000, 1000) == 10
+    assert vk.pick_version(1000, 1000, 1000) == 11  # 64 tiles of 128 x 128 with edges
+    assert vk.pick_version(2600, 2600, 72) == 10    # 441 tiles of 128 x 128: over 1.5 waves
     assert vk.pick_version(512, 512, 512, "f32") == 2   # fp32 on the matrix cores
     assert vk.pick_version(500, 512, 512, "f32") == 3   # m % 256 != 0: the matrix cores with edges
     assert vk.pick_version(500, 510, 512, "f32") == 1   # n % 4 != 0: the VALU kernel

@@ -1,5 +1,7 @@
 """GPU parity of version 10 -- version 7's kernel for shapes off its
-256 x 256 x 64 grid (any M; N and K multiples of 8) -- through the C ABI.
+256 x 256 x 64 grid (any M; N and K multiples of 8) -- and of version 11's
+edge tiles (128 x 128 tiles off their grid, the same treatment) through the
+C ABI.
 
 * On the grid it runs version 7's arithmetic in version 7's order: bitwise
   equal results.
@@ -33,9 +35,10 @@ def test_on_grid_equals_v7(gpu, shape, out):
                           C10.view(np.uint16 if out == "f16" else np.uint32))
 
 
+@pytest.mark.parametrize("version", [10, 11])
 @pytest.mark.parametrize("shape", [(300, 264, 72), (1, 8, 8), (257, 1000, 512), (600, 40, 1032), (257, 520, 4096)])
 @pytest.mark.parametrize("out", ["f16", "f32"])
-def test_writes_only_c(gpu, shape, out):
+def test_writes_only_c(gpu, shape, out, version):
     """C sits between two 4096-element guard regions of NaN; integer inputs
     in [-2, 2] with k <= 1032 keep every sum exact in fp32 and, up to 2048,
     in fp16."""
@@ -50,15 +53,16 @@ def test_writes_only_c(gpu, shape, out):
     dt = torch.float16 if out == "f16" else torch.float32
     buf = torch.full((pad + m * n + pad,), float("nan"), dtype=dt, device="cuda:0")
     C = buf[pad:pad + m * n].view(m, n)
-    announce(f"version=10 guarded m={m} n={n} k={k} out={out}")
-    vk.matmul(m, n, k, torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda(), C, 10)
+    announce(f"version={version} guarded m={m} n={n} k={k} out={out}")
+    vk.matmul(m, n, k, torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda(), C, version)
     torch.cuda.synchronize()
     assert torch.isnan(buf[:pad]).all() and torch.isnan(buf[pad + m * n:]).all()
     assert np.array_equal(C.cpu().numpy().astype(np.int64), exact)
 
 
+@pytest.mark.parametrize("version", [10, 11])
 @pytest.mark.parametrize("out", ["f16", "f32"])
-def test_values_past_the_edges_never_reach_c(gpu, out):
+def test_values_past_the_edges_never_reach_c(gpu, out, version):
     """M = 3, N = 8, K = 72: row 0's last k-tile covers k = 64..127, and
     k = 72..79 of row 0 is, in memory, A[1][0..7]; columns 8..15 of B's row r
     are B[r+1][0..7].  With A[1][0] and B[5][0] infinite, row 1 and column 0
@@ -67,7 +71,7 @@ def test_values_past_the_edges_never_reach_c(gpu, out):
     A, B = make_inputs(m, n, k, "int", seed=72)
     A[1, 0] = np.inf
     B[5, 0] = np.inf
-    C = run_gemm(10, A, B, out).astype(np.float64)
+    C = run_gemm(version, A, B, out).astype(np.float64)
     with np.errstate(invalid="ignore"):
         exact = A.astype(np.float64) @ B.astype(np.float64)
     keep = np.ones((m, n), dtype=bool)
@@ -77,14 +81,15 @@ def test_values_past_the_edges_never_reach_c(gpu, out):
     assert np.array_equal(C[keep], exact[keep])
 
 
+@pytest.mark.parametrize("version", [10, 11])
 @pytest.mark.parametrize("shape", [(1000, 1000, 1000), (4096, 4096, 4128), (2000, 3000, 1000), (1000, 1000, 4000),
                                    (257, 520, 4096), (1496, 1496, 3000)])
-def test_ragged_random_vs_oracle(gpu, oracle, shape):
+def test_ragged_random_vs_oracle(gpu, oracle, shape, version):
     m, n, k = shape
     A, B = make_inputs(m, n, k, "uniform", seed=10 + m + k)
     C64 = oracle.dgemm(A, B)
-    check_f32_out(run_gemm(10, A, B, "f32"), A, B, C64)
-    C16 = run_gemm(10, A, B, "f16")
+    check_f32_out(run_gemm(version, A, B, "f32"), A, B, C64)
+    C16 = run_gemm(version, A, B, "f16")
     check_f16_out(C16, A, B, C64)
     err, st = oracle.mean_rel_err(oracle.hgemm(A, B), C16)
     assert st == oracle.STATUS_OK and err < 2e-4
@@ -142,7 +147,7 @@ def test_split_caller_workspace(gpu):
         assert np.array_equal(tC.cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("version,dtype", [(10, "f16"), (3, "f32")])
+@pytest.mark.parametrize("version,dtype", [(10, "f16"), (11, "f16"), (3, "f32")])
 @pytest.mark.parametrize("shape", [(3, 8, 72), (17, 40, 200), (300, 264, 104)])
 def test_memory_past_the_operands_is_never_read(gpu, version, dtype, shape):
     """A and B are views at the start of larger buffers whose elements past

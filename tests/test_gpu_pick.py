@@ -17,9 +17,10 @@ F16_CASES = [
     ((512, 512, 512), 11),       # 16 tiles of 128 x 128 where 256 x 256 gives 4 (and no split)
     ((2048, 2048, 4096), 11),    # 256 tiles of 128 x 128: one wave
     ((1024, 1024, 8192), 9),     # 64 tiles of 128 x 128: the split tail of 16 large tiles
-    ((300, 264, 72), 10),        # off the grid
-    ((1000, 1000, 4000), 10),    # off the grid, split tail
-    ((512, 512, 544), 10),       # k % 64 != 0
+    ((300, 264, 72), 11),        # off the grid: 128 x 128 tiles with edges
+    ((1000, 1000, 4000), 11),    # off the grid, 64 tiles of 128 x 128
+    ((512, 512, 544), 11),       # k % 64 != 0
+    ((2600, 2600, 72), 10),      # off the grid, 441 tiles of 128 x 128: 256 x 256 tiles with edges
     ((100, 300, 70), 1),         # n % 8 != 0: any shape
 ]
 F32_CASES = [

@@ -10,7 +10,13 @@ Bars:
 * fp32 and fp16 output against the exact product within the fp32
   accumulation bound (fp16: plus half an fp16 ulp), every element written
   (C poisoned with NaN), on shapes version 7 does not take;
-* small-integer inputs bit-exact against the oracle.
+* small-integer inputs bit-exact against the oracle;
+* off the 128 x 128 x 128 grid (edge tiles: any M, N and K multiples of 8)
+  bitwise equal to version 10 where version 10 runs whole tiles: both sum
+  each element over the same 32-deep k-steps with zero padding past K (a
+  128-deep boundary adds exact zeros to the 64-deep one); the
+  guard, past-the-edge and past-the-allocation tests of version 10 cover
+  version 11 too (tests/test_gpu_edge.py).
 """
 import numpy as np
 import pytest
@@ -62,3 +68,19 @@ def test_repeat_launch_deterministic(gpu):
         vk.matmul(m, n, k, tA, tB, C, 11)
     torch.cuda.synchronize()
     assert torch.equal(C.view(torch.int16), ref.view(torch.int16))
+
+
+@pytest.mark.parametrize("out", ["f16", "f32"])
+@pytest.mark.parametrize("shape", [(1, 8, 8), (100, 264, 136), (257, 520, 200), (1000, 4096, 448), (3000, 1000, 520),
+                                   (129, 136, 256)])
+def test_edges_bitwise_equal_version10(gpu, shape, out):
+    """K <= 448 (at most 7 k-tiles of 64): version 10's split-tail plan never
+    splits (a piece needs 8), so it runs whole tiles, one chain per element."""
+    import vibekernel_amd as vk
+    m, n, k = shape
+    assert vk._abi.workspace_bytes(10, vk._abi.DTYPE_F16, m, n, k) == 0
+    A, B = make_inputs(m, n, k, "uniform", seed=m + 5 * n + 3 * k)
+    C11 = run_gemm(11, A, B, out)
+    C10 = run_gemm(10, A, B, out)
+    bits = np.uint16 if out == "f16" else np.uint32
+    assert np.array_equal(C11.view(bits), C10.view(bits))

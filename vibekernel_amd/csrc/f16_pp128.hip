@@ -32,7 +32,14 @@
 //  * the epilogue stages each wave's 64x32 block of C through LDS (8-byte
 //    units XOR 2 ((row / 4) % 4) for fp16, 16-byte chunks XOR (row / 2) % 8
 //    for fp32) and stores 16-byte pieces of full row segments.
-// M, N and K multiples of 128.
+// Shapes: any M, N and K multiples of 8.  Off the 128 x 128 x 128 grid the
+// edge tiles and the last k-tile reach past the matrices (kEdge, version
+// 10's treatment): the loads go through buffer resources over the whole
+// matrices, which return zeros past a matrix's end (A rows at or below M, B
+// k-rows at or below K); A's k past K on the last k-tile (the next row's
+// values, which must not meet B's zero rows: an infinity would make a NaN)
+// is masked by a select; B columns past N only feed C columns that are not
+// stored; the C stores are bounds-checked.
 #include "vk_device.hpp"
 #include "vk_internal.hpp"
 #include "vk_tile.hpp"
@@ -89,6 +96,19 @@ struct Epi<half_t> {
       *reinterpret_cast<uint4v*>(Cw + (size_t)row * N + ch * 8) = v;
     }
   }
+  // The block at (row0, col0) of C may reach past M rows or N columns (N a
+  // multiple of 8): chunks outside are not stored.
+  static __device__ __forceinline__ void store_edge(uint32_t wbase, half_t* C, int M, int N, int row0, int col0,
+                                                    int lane) {
+    const int rsub = lane >> 2, ch = lane & 3;
+    const bool col_in = col0 + ch * 8 < N;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const int row = 16 * q + rsub;
+      const uint4v v = lds_read16(wbase + row * 64 + 16 * (ch ^ (swz(row) >> 1)));
+      if (col_in && row0 + row < M) *reinterpret_cast<uint4v*>(C + (size_t)(row0 + row) * N + col0 + ch * 8) = v;
+    }
+  }
 };
 
 // fp32: rows of 128 B = 8 chunks of 16 B (4 floats); chunk u of row r at
@@ -109,9 +129,20 @@ struct Epi<float> {
       *reinterpret_cast<uint4v*>(Cw + (size_t)row * N + ch * 4) = v;
     }
   }
+  static __device__ __forceinline__ void store_edge(uint32_t wbase, float* C, int M, int N, int row0, int col0,
+                                                    int lane) {
+    const int rsub = lane >> 3, ch = lane & 7;
+    const bool col_in = col0 + ch * 4 < N;
+#pragma unroll
+    for (int q = 0; q < 8; q++) {
+      const int row = 8 * q + rsub;
+      const uint4v v = lds_read16(wbase + row * 128 + 16 * (ch ^ ((row >> 1) & 7)));
+      if (col_in && row0 + row < M) *reinterpret_cast<uint4v*>(C + (size_t)(row0 + row) * N + col0 + ch * 4) = v;
+    }
+  }
 };
 
-template <typename OutT>
+template <typename OutT, bool kEdge>
 __global__ __launch_bounds__(kThreads) void f16_pp128_kernel(const half_t* __restrict__ A,
                                                              const half_t* __restrict__ B,
                                                              OutT* __restrict__ C, int M, int N, int K) {
@@ -120,10 +151,11 @@ __global__ __launch_bounds__(kThreads) void f16_pp128_kernel(const half_t* __res
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = wave >> 2;  // 0 = P, 1 = Q; waves w and w+4 share a SIMD
   const int gw = wave & 3;
+  constexpr int kR = kEdge ? 1 : 0;  // round the tile and k-tile counts up
   int tm, tn;
-  tile_of(blockIdx.x, M / kBM, N / kBN, tm, tn);
+  tile_of(blockIdx.x, (M + kR * (kBM - 1)) / kBM, (N + kR * (kBN - 1)) / kBN, tm, tn);
   const int m0 = tm * kBM, n0 = tn * kBN;
-  const int nk = K / kBK;
+  const int nk = (K + kR * (kBK - 1)) / kBK;
   const uint32_t lds_base = lds_addr32(lds);
 
   // ---- direct-to-LDS duty: instruction d = 4h + i (8 per wave per k-tile) ----
@@ -155,11 +187,35 @@ __global__ __launch_bounds__(kThreads) void f16_pp128_kernel(const half_t* __res
   const uint32_t l_slot = grp ? (uint32_t)kHalfBytes : (uint32_t)kBBytes;  // per slot
   const uint32_t l_h = grp ? (uint32_t)(kABot - kATop) : 16u * kBRowBytes;  // per h
 
+  // Edges: the same loads through a buffer resource over the whole matrix
+  // (below 2^31 bytes), the k-tile's offset in the scalar offset and the
+  // lane's within the k-tile in the VGPR, so a lane past the end of the
+  // matrix reads zeros.  Byte 8i of akin (Q): the first k of the lane's A
+  // chunk in instruction i within a k-tile; a chunk at or past K gets the
+  // matrix size as its offset (zeros).
+  uint32_t akin = 0;
+  if constexpr (kEdge) {
+    if (grp) {
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const int row = gw * 16 + 4 * i + (lane >> 4);
+        akin |= (uint32_t)(((lane & 15) ^ swz_a(row)) * 8) << (8 * i);
+      }
+    }
+  }
+  const char* g_start = grp ? reinterpret_cast<const char*>(A) : reinterpret_cast<const char*>(B);
+  const uint32_t g_size = kEdge ? (uint32_t)(grp ? (size_t)M * K * 2 : (size_t)K * N * 2) : 0u;
+  const __amdgpu_buffer_rsrc_t g_rsrc =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<char*>(g_start), 0, (int)g_size, kBufferWord3);
+  const uint32_t g_off0 = (uint32_t)(g_base - g_start);  // kEdge: below 2^31
+
   // Scalar operands of the 8 loads of one k-tile, computed in the memory
   // phase so that the compute phase issues each load as M0, its wait state
   // and the load between two MFMAs.
   struct DmaOps {
-    const char* g[2];  // global base of half h
+    const char* g[2];  // global base of half h (kEdge: unused)
+    uint32_t soff[2];  // kEdge: the buffer's scalar offset of half h
+    uint32_t kleft;    // kEdge: k from the k-tile's start to K (Q), 128 (P)
     uint32_t l[8];     // LDS destination of load d
   };
   auto dma_ops = [&](int kt, int slot) {
@@ -167,18 +223,33 @@ __global__ __launch_bounds__(kThreads) void f16_pp128_kernel(const half_t* __res
     const uint32_t ls = l_base + slot * l_slot;
 #pragma unroll
     for (int h = 0; h < 2; h++) {
-      o.g[h] = g_base + (size_t)kt * g_kt + h * g_h;
+      if constexpr (kEdge)
+        o.soff[h] = g_off0 + (uint32_t)kt * (uint32_t)g_kt + (uint32_t)h * (uint32_t)g_h;
+      else
+        o.g[h] = g_base + (size_t)kt * g_kt + h * g_h;
 #pragma unroll
       for (int i = 0; i < 4; i++) o.l[4 * h + i] = ls + h * l_h + i * 1024;
     }
+    o.kleft = kEdge && grp ? (uint32_t)(K - kt * kBK) : (uint32_t)kBK;
     return o;
   };
   auto pin_ops = [&](const DmaOps& o) {
-    asm volatile("" ::"s"(o.g[0]), "s"(o.g[1]));
+    if constexpr (kEdge)
+      asm volatile("" ::"s"(o.soff[0]), "s"(o.soff[1]), "s"(o.kleft));
+    else
+      asm volatile("" ::"s"(o.g[0]), "s"(o.g[1]));
     asm volatile("" ::"s"(o.l[0]), "s"(o.l[1]), "s"(o.l[2]), "s"(o.l[3]), "s"(o.l[4]), "s"(o.l[5]), "s"(o.l[6]),
                  "s"(o.l[7]));
   };
-  auto dma_with = [&](int d, const DmaOps& o) { dma16(o.g[d >> 2], voff[d & 3], o.l[d]); };
+  auto dma_with = [&](int d, const DmaOps& o) {
+    const int i = d & 3, h = d >> 2;
+    if constexpr (kEdge) {
+      const uint32_t off = ((akin >> (8 * i)) & 255u) < o.kleft ? voff[i] : g_size;  // g_size: zeros
+      dma16_buf(g_rsrc, off, o.soff[h], o.l[d]);
+    } else {
+      dma16(o.g[h], voff[i], o.l[d]);
+    }
+  };
   auto dma = [&](int d, int kt, int slot) { dma_with(d, dma_ops(kt, slot)); };
 
   // ---- fragment addresses ----
@@ -294,30 +365,40 @@ __global__ __launch_bounds__(kThreads) void f16_pp128_kernel(const half_t* __res
 #pragma unroll
     for (int j = 0; j < 2; j++) Epi<OutT>::stage(wstage, lane, i, j, acc[i][j]);
   wait_lgkmcnt0();  // a wave reads back only its own region
-  Epi<OutT>::store(wstage, C + (size_t)(m0 + grp * 64) * N + n0 + gw * 32, N, lane);
+  if constexpr (kEdge)
+    Epi<OutT>::store_edge(wstage, C, M, N, m0 + grp * 64, n0 + gw * 32, lane);
+  else
+    Epi<OutT>::store(wstage, C + (size_t)(m0 + grp * 64) * N + n0 + gw * 32, N, lane);
 }
 
-template <typename OutT>
+template <typename OutT, bool kEdge>
 hipError_t launch_t(const GemmArgs& a) {
   static std::atomic<uint64_t> attr_done{0};
-  auto kfn = f16_pp128_kernel<OutT>;
+  auto kfn = f16_pp128_kernel<OutT, kEdge>;
   hipError_t e = ensure_lds_attr(kfn, kLdsBytes, a.device, attr_done);
   if (e != hipSuccess) return e;
-  const int tiles = (int)((a.m / kBM) * (a.n / kBN));
+  const size_t r = kEdge ? 1 : 0;
+  const int tiles = (int)(((a.m + r * (kBM - 1)) / kBM) * ((a.n + r * (kBN - 1)) / kBN));
   hipLaunchKernelGGL(kfn, dim3(tiles), dim3(kThreads), kLdsBytes, a.stream, static_cast<const half_t*>(a.A),
                      static_cast<const half_t*>(a.B), static_cast<OutT*>(a.C), (int)a.m, (int)a.n, (int)a.k);
   return hipGetLastError();
 }
 
+// Shapes on the 128 x 128 x 128 grid run without the edge treatment.
 hipError_t launch(const GemmArgs& a) {
-  return a.out_dtype == VK_DTYPE_F16 ? launch_t<half_t>(a) : launch_t<float>(a);
+  const bool grid = a.m % kBM == 0 && a.n % kBN == 0 && a.k % kBK == 0;
+  if (a.out_dtype == VK_DTYPE_F16) return grid ? launch_t<half_t, false>(a) : launch_t<half_t, true>(a);
+  return grid ? launch_t<float, false>(a) : launch_t<float, true>(a);
 }
 
-// 32-bit lane offsets (64 rows of A, 128 k-rows of B past the scalar base)
-// and the 1-D grid.
+// 32-bit lane offsets (64 rows of A, 128 k-rows of B past the scalar base),
+// each operand below 2^31 bytes with room for the last tile's rows and
+// k-rows past it (buffer sizes; scalar plus lane offsets of the edge
+// tiles), and the 1-D grid.
 bool shape_ok(size_t m, size_t n, size_t k) {
-  return (size_t)kBM * k * 2 < (1ull << 31) && (size_t)kBK * n * 2 < (1ull << 31) &&
-         (m / kBM) * (n / kBN) < (1ull << 31);
+  return m >= 1 && n >= 8 && k >= 8 && (size_t)kBM * k * 2 < (1ull << 31) && (size_t)kBK * n * 2 < (1ull << 31) &&
+         (m + 2 * kBM) * k * 2 < (1ull << 31) && (k + 2 * kBK) * n * 2 < (1ull << 31) &&
+         ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN) < (1ull << 31);
 }
 
 }  // namespace pp128
@@ -328,7 +409,7 @@ void register_f16_pp128() {
   e.version = 11;
   e.in_dtype = VK_DTYPE_F16;
   e.name = "f16_v11_pp128_bk128";
-  e.caps = make_caps(11, VK_DTYPE_F16, kOutF16 | kOutF32, pp128::kBM, pp128::kBN, pp128::kBK, 16, pp128::kBM,
+  e.caps = make_caps(11, VK_DTYPE_F16, kOutF16 | kOutF32, 1, 8, 8, 16, pp128::kBM,
                      pp128::kBN, pp128::kBK, pp128::kThreads, pp128::kLdsBytes, 0, 0);
   e.launch = pp128::launch;
   e.workspace = nullptr;

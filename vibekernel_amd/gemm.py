@@ -113,17 +113,25 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
     """The fastest version that accepts this shape (checked with vk_gemm_check
     on 4 KiB-aligned placeholder addresses; nothing is launched): for fp16
     the skinny kernels when M <= 256 (64 for version 4), then the 128 x 128
-    tiles of version 11 where they make one wave of the compute units and
-    either fill more than a quarter of them or the split-tail plan splits
-    nothing (measured on MI355X: 1024 x 4096 x 4096 33.6 us against 46.2 for
-    version 9 and 64.5 for version 7; 1024 x 1024 x 8192, 64 such tiles,
-    47.3 against version 9's 43.9), then the 256x256 kernels (fastest first;
-    version 10 takes shapes off the 256 x 256 x 64 grid whose N and K are
-    multiples of 8), then the any-shape kernel.  The split-tail version 9
-    comes first among the 256x256 kernels only where its schedule splits
-    tiles on this device (it then needs a workspace); elsewhere it would run
-    version 7's whole tiles.  The reference picks versions at build time only
-    (CMakeLists.txt MATMUL_VERSION); this is a convenience of the front end."""
+    tiles of version 11 where they suit the grid, then the 256x256 kernels
+    (fastest first; version 10 takes shapes off the 256 x 256 x 64 grid
+    whose N and K are multiples of 8), then the any-shape kernel.  Version 11
+    is taken, with T its 128 x 128 tiles on C compute units:
+      * on the 256 x 256 x 64 grid, where T <= C and either 4 T > C or the
+        split-tail plan of version 9 splits nothing (measured on MI355X:
+        1024 x 4096 x 4096 33.6 us against 46.2 for version 9 and 64.5 for
+        version 7; 1024 x 1024 x 8192, T = 64, 47.3 against version 9's
+        43.9; 1536 x 4096 x 4096, T = 384, 58.7 against 50.6);
+      * off it, where T <= 3 C / 2 (version 10, whose split pieces do not stay
+        on one XCD there and whose edge tiles are twice as wide, measured
+        slower on every such shape: 1000 x 1000 x 1000 23.0 us against 9.8,
+        2000 x 3000 x 1000 (T = 384) 25.2 against 21.2, 1000 x 1000 x 4000
+        (T = 64) 36.7 against 29.2).
+    The split-tail version 9 comes first among the 256x256 kernels only where
+    its schedule splits tiles on this device (it then needs a workspace);
+    elsewhere it would run version 7's whole tiles.  The reference picks
+    versions at build time only (CMakeLists.txt MATMUL_VERSION); this is a
+    convenience of the front end."""
     in_dt = DTYPE_F16 if dtype == "f16" else DTYPE_F32
     out_dt = DTYPE_F16 if (out or dtype) == "f16" else DTYPE_F32
     order = [8, 4, 11, 9, 7, 10, 6, 5, 3, 2, 1] if in_dt == DTYPE_F16 else [2, 3, 1]
@@ -136,9 +144,12 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
             continue
         if v == 11:
             cus = cus or _num_cus()
-            tiles = (m // 128) * (n // 128)
-            splits = 9 in avail and _abi.workspace_bytes(9, in_dt, m, n, k) > 0
-            if not (tiles <= cus and (4 * tiles > cus or not splits)):
+            tiles = -(-m // 128) * -(-n // 128)
+            if m % 256 == 0 and n % 256 == 0 and k % 64 == 0:
+                splits = 9 in avail and _abi.workspace_bytes(9, in_dt, m, n, k) > 0
+                if not (tiles <= cus and (4 * tiles > cus or not splits)):
+                    continue
+            elif 2 * tiles > 3 * cus:
                 continue
         if _abi.check(v, in_dt, out_dt, m, n, k, 4096, 4096, 4096) == _abi.VK_OK:
             return v
