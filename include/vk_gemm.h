@@ -106,7 +106,8 @@ int vk_gemm_ws(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m, siz
 /* Size of the device scratch array behind vk_gemm_noalloc: the largest
  * workspace any version plans on a device of up to 256 CUs (version 9's 256
  * split-tail pieces of 256 KiB plus their counters; version 8's split-K
- * partials stay within 32 MiB), with room to spare. */
+ * partials stay within 32 MiB, version 11's k-slices within 16 MiB), with
+ * room to spare. */
 #define VK_GEMM_SCRATCH_BYTES ((size_t)64 * 1024 * 1024 + (size_t)64 * 1024)
 
 /* Same as vk_gemm, but allocates nothing (no hipMalloc or hipFree, no host
@@ -123,7 +124,8 @@ int vk_gemm_noalloc(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m
                     const void* A, const void* B, void* C, void* stream);
 
 /* Workspace bytes a call of this version and shape needs on the current
- * device (0: none).  Versions 8 and 9 depend on the device's compute-unit count;
+ * device (0: none).  Versions 8, 9, 10 and 11 depend on the device's
+ * compute-unit count;
  * with no device to ask, an MI355X's 256 CUs are assumed.  No counterpart in
  * the reference, whose versions keep such buffers in function-local statics
  * (matmul_f16_v42_shfl2.cu:496-519). */

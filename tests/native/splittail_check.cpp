@@ -1,8 +1,9 @@
-// Host-side check of version 9's tail schedule (vk_splittail.hpp): simulates
-// every workgroup of a launch for many tile counts, k-depths and CU counts --
-// for the plan sk_plan chooses and for every other admissible piece count --
-// and checks that the pieces cover each (tile, k-iteration) exactly once and
-// that the pieces of a split tile agree on where they meet.
+// Host-side check of version 9's tail schedule and version 11's split of
+// under-filled grids (vk_splittail.hpp): simulates every workgroup of a
+// launch for many tile counts, k-depths and CU counts -- for the plan sk_plan
+// (or sk_plan_fill) chooses and, for sk_plan, every other admissible piece
+// count -- and checks that the pieces cover each (tile, k-iteration) exactly
+// once and that the pieces of a split tile agree on where they meet.
 // Prints "ok <cases> <split plans>" or the first violation; exit status 1 on a
 // violation.
 #include "vk_splittail.hpp"
@@ -19,14 +20,14 @@ static int fail(const char* what, int tm, int tn, int I, int C, const SkPlan& p)
   return 1;
 }
 
-static int check_plan(int tiles_m, int tiles_n, int I, int C, const SkPlan& p) {
+static int check_plan(int tiles_m, int tiles_n, int I, int C, const SkPlan& p, int extra = kSkLastExtra) {
   const int T = tiles_m * tiles_n;
   const int grid = p.dp + p.units;
   std::vector<int> cover((size_t)T * I, 0);
   std::set<std::pair<int, int>> tiles_seen;
   std::vector<SkWork> work(grid);
   for (int bid = 0; bid < grid; bid++) {
-    const SkWork w = sk_work(bid, T, I, p);
+    const SkWork w = sk_work(bid, T, I, p, extra);
     work[bid] = w;
     if (w.cid < 0 || w.cid >= T || w.kb < 0 || w.ke > I || w.kb >= w.ke) return fail("work range", tiles_m, tiles_n, I, C, p);
     for (int k = w.kb; k < w.ke; k++) cover[(size_t)w.cid * I + k]++;
@@ -39,9 +40,9 @@ static int check_plan(int tiles_m, int tiles_n, int I, int C, const SkPlan& p) {
       continue;
     }
     if (w.np != p.pieces || w.p < 0 || w.p >= w.np) return fail("piece index", tiles_m, tiles_n, I, C, p);
-    if (w.ke - w.kb < (I - kSkLastExtra) / p.pieces || w.ke - w.kb < 1)
+    if (w.ke - w.kb < (I - extra) / p.pieces || w.ke - w.kb < 1)
       return fail("piece shorter than (I - extra) / pieces", tiles_m, tiles_n, I, C, p);
-    if (w.p == w.np - 1 && w.ke - w.kb < (I - kSkLastExtra) / p.pieces + kSkLastExtra)
+    if (w.p == w.np - 1 && w.ke - w.kb < (I - extra) / p.pieces + extra)
       return fail("last piece without its extra iterations", tiles_m, tiles_n, I, C, p);
     if ((size_t)(w.tile + 1) * kSkWaves > kSkCounterBytes / sizeof(unsigned)) return fail("counter out of range", tiles_m, tiles_n, I, C, p);
     if (sk_unit_of(p, T, w.tile, w.p) != bid - p.dp) return fail("unit_of(own piece) != self", tiles_m, tiles_n, I, C, p);
@@ -104,6 +105,31 @@ int main() {
             forced++;
           }
         }
+  // Version 11's split of under-filled grids.
+  long long fill_plans = 0;
+  for (int tiles_m = 1; tiles_m <= 24; tiles_m++)
+    for (int tiles_n = 1; tiles_n <= 48; tiles_n += (tiles_n < 16 ? 1 : 5))
+      for (int I : Is)
+        for (int C : Cs) {
+          const int T = tiles_m * tiles_n;
+          const SkPlan p = sk_plan_fill(T, I, C);
+          const int Cc = C < kSkMaxUnits ? C : kSkMaxUnits;
+          if (p.units == 0) {
+            if (p.dp != T || p.pieces != 1) return fail("fill: whole plan", tiles_m, tiles_n, I, C, p);
+            if (2 * T <= Cc && Cc / T >= 2 && I / kFillMinIters >= 2) return fail("fill: split missed", tiles_m, tiles_n, I, C, p);
+            continue;
+          }
+          fill_plans++;
+          if (p.dp != 0 || p.units != p.pieces * T || p.units > Cc || p.pieces < 2 || p.pieces > kFillMaxPieces ||
+              I / p.pieces < kFillMinIters || p.chunks != (T % 8 == 0 ? 8 : 1))
+            return fail("fill: plan shape", tiles_m, tiles_n, I, C, p);
+          if (check_plan(tiles_m, tiles_n, I, C, p, kFillLastExtra)) return 1;
+          cases++;
+        }
+  if (fill_plans == 0) {
+    std::printf("FAIL no fill plan split anything\n");
+    return 1;
+  }
   // Plans the GPU tests rely on (256 CUs).
   struct Want { int T, I, dp, units, pieces, chunks; } wants[] = {
       {16 * 43, 64, 688, 0, 1, 1},    // 4096 x 11008 x 4096: 176 of 256 busy, left whole
@@ -119,6 +145,23 @@ int main() {
       return 1;
     }
   }
-  std::printf("ok %lld cases, %lld split plans, %lld forced piece counts\n", cases, split_plans, forced);
+  struct WantFill { int T, I, units, pieces, chunks; } fills[] = {
+      {4 * 32, 32, 256, 2, 8},  // 512 x 4096 x 4096
+      {8 * 8, 32, 256, 4, 8},   // 1000 x 1000 x 4000
+      {1 * 16, 18, 32, 2, 8},   // 128 x 2048 x 2304
+      {3 * 5, 64, 120, 8, 1},   // 384 x 640 x 8192
+      {2 * 3, 16, 12, 2, 1},    // 200 x 296 x 2000
+      {8 * 8, 8, 0, 1, 1},      // 1000^3: 8 k-tiles, left whole
+      {16 * 16, 32, 0, 1, 1},   // 2048 x 2048 x 4096: one full wave
+  };
+  for (const WantFill& w : fills) {
+    const SkPlan p = sk_plan_fill(w.T, w.I, 256);
+    if (p.units != w.units || p.pieces != w.pieces || (p.units && p.chunks != w.chunks)) {
+      std::printf("FAIL fill plan for T %d I %d: units %d pieces %d chunks %d\n", w.T, w.I, p.units, p.pieces, p.chunks);
+      return 1;
+    }
+  }
+  std::printf("ok %lld cases, %lld split plans, %lld forced piece counts, %lld fill plans\n", cases, split_plans,
+              forced, fill_plans);
   return 0;
 }

@@ -146,7 +146,8 @@ def test_pick_version_follows_shape():
     assert vk.pick_version(4096, 11008, 4096) == 7  # 688 tiles = 2.69 waves: tail left whole
     assert vk.pick_version(2048, 2048, 4096) == 11  # 64 tiles of 256 x 256, 256 of 128 x 128: one wave
     assert vk.pick_version(512, 512, 512) == 11     # 16 tiles of 128 x 128 where 256 x 256 gives 4, no split
-    assert vk.pick_version(1024, 1024, 8192) == 9   # 64 tiles of 128 x 128: the split tail of 16 large tiles
+    assert vk.pick_version(1024, 1024, 8192) == 11  # 64 tiles of 128 x 128, K split 4 ways over the idle CUs
+    assert vk.pick_version(512, 512, 8192) == 11    # 16 tiles of 128 x 128, K split 8 ways
     assert vk.pick_version(3840, 4096, 4096) == 7   # 240 of 256 CUs busy: not worth a split
     assert vk.pick_version(4096, 4096, 4128) == 10  # k % 64 != 0: v7 with a masked last k-tile
     assert vk.pick_version(100, 300, 70) == 1

@@ -148,13 +148,14 @@ def test_split_caller_workspace(gpu):
 
 
 @pytest.mark.parametrize("version,dtype", [(10, "f16"), (11, "f16"), (3, "f32")])
-@pytest.mark.parametrize("shape", [(3, 8, 72), (17, 40, 200), (300, 264, 104)])
+@pytest.mark.parametrize("shape", [(3, 8, 72), (17, 40, 200), (300, 264, 104), (100, 136, 2056)])
 def test_memory_past_the_operands_is_never_read(gpu, version, dtype, shape):
     """A and B are views at the start of larger buffers whose elements past
     the matrices are +inf: the last k-tile's B rows past K and the A rows past
     M lie beyond the allocations' matrix bytes, and the loads through buffer
     resources sized to the matrices must return zeros there (K % 64 != 0 and
-    M, N off the tile grid).  Every C element is finite and exact."""
+    M, N off the tile grid; 100 x 136 x 2056 also splits K under version
+    11).  Every C element is finite and exact."""
     import torch
     import vibekernel_amd as vk
     m, n, k = shape

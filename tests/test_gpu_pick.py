@@ -16,7 +16,8 @@ F16_CASES = [
     ((4096, 4096, 256), 7),      # one full wave of 256 x 256 tiles
     ((512, 512, 512), 11),       # 16 tiles of 128 x 128 where 256 x 256 gives 4 (and no split)
     ((2048, 2048, 4096), 11),    # 256 tiles of 128 x 128: one wave
-    ((1024, 1024, 8192), 9),     # 64 tiles of 128 x 128: the split tail of 16 large tiles
+    ((1024, 1024, 8192), 11),    # 64 tiles of 128 x 128: K split 4 ways over the idle CUs
+    ((2048, 2304, 4096), 9),     # 288 tiles of 128 x 128; 72 of 256 x 256, each cut in 3 k-slices
     ((300, 264, 72), 11),        # off the grid: 128 x 128 tiles with edges
     ((1000, 1000, 4000), 11),    # off the grid, 64 tiles of 128 x 128
     ((512, 512, 544), 11),       # k % 64 != 0

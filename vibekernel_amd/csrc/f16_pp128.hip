@@ -40,8 +40,11 @@
 // values, which must not meet B's zero rows: an infinity would make a NaN)
 // is masked by a select; B columns past N only feed C columns that are not
 // stored; the C stores are bounds-checked.
+// Where the tiles fill at most half of the CUs, K is split over the idle
+// ones (kSplit, below), the pieces meeting through fp32 partials.
 #include "vk_device.hpp"
 #include "vk_internal.hpp"
+#include "vk_splittail.hpp"
 #include "vk_tile.hpp"
 
 #include <atomic>
@@ -142,20 +145,126 @@ struct Epi<float> {
   }
 };
 
-template <typename OutT, bool kEdge>
+// ---- split K for grids whose tiles fill at most half of the CUs ----
+// With T tiles of I k-tiles on C CUs and 2T <= C, each tile is cut into
+// s = min(8, C / T, I / 4) aligned k-slices (at least 4 k-tiles each)
+// computed by s workgroups at once (sk_plan_fill in vk_splittail.hpp: no
+// whole tiles; the pieces of an XCD's share of the raster stay on it), and
+// the pieces of a tile meet as in version 9: per (tile, wave) an arrival
+// counter; a finishing wave that finds every other piece in memory is the
+// last and writes nothing, otherwise it writes its 8 KB fp32 partial with
+// sc1 stores, waits for them and increments the counter, and the one that
+// sees s - 1 is the last.  The last sums P0 + P1 + ... in k order (its own
+// piece from registers), so C does not depend on the arrival order, stores
+// C and resets the counter.  The last piece is one k-tile longer than the
+// others, so it usually arrives last and skips its store.
+constexpr size_t kSlotBytes = (size_t)kBM * kBN * sizeof(float);  // one tile's fp32 partial
+constexpr uint32_t kWaveSlotBytes = 64 * 32 * 4;                   // a wave's 64x32 block
+
+// This wave holds piece p of np of its block.  part_off(q): byte offset of
+// the wave's region of piece q's slot (8 blocks x 64 lanes x 16 bytes, each
+// access a coalesced 1 KB row).  Returns whether this wave arrived last.
+// Only the last piece, which usually arrives last, reads the counter first;
+// the others publish their partial at once.
+template <typename PartOff>
+__device__ __forceinline__ bool split_arrive(const float4v (&acc)[4][2], int np, int p, int lane,
+                                             __amdgpu_buffer_rsrc_t part, PartOff part_off, unsigned* cnt) {
+  if (p == np - 1) {
+    const unsigned seen =
+        __builtin_amdgcn_readfirstlane(__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    if (seen == (unsigned)(np - 1)) return true;  // every other piece is in memory
+  }
+  const uint32_t soff = part_off(p);
+#pragma unroll
+  for (int b = 0; b < 8; b++) store_partial(part, (uint32_t)lane * 16 + b * 1024, soff, acc[b >> 1][b & 1]);
+  wait_vmcnt0_ordered();  // the partial is in memory before the counter moves
+  unsigned old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __builtin_amdgcn_readfirstlane(old) == (unsigned)(np - 1);
+}
+
+// The last arrival: acc <- P0 + P1 + ... + P(NP-1), left to right, P(p) =
+// acc.  The partials' loads go out together, kB blocks of every piece at a
+// time (at most 32 loads in flight: 128 registers), so the wait is one
+// memory round trip per batch (measured ~1.2 us each); the own piece's slot
+// is loaded too and not used (no branch; the slot is always inside the
+// workspace).
+template <int NP, typename PartOff>
+__device__ __forceinline__ void split_sum_n(float4v (&acc)[4][2], int p, int lane, __amdgpu_buffer_rsrc_t part,
+                                            PartOff part_off) {
+  constexpr int kB = NP <= 4 ? 8 : 4;  // blocks per batch
+#pragma unroll
+  for (int b0 = 0; b0 < 8; b0 += kB) {
+    float4v x[NP][kB];
+#pragma unroll
+    for (int q = 0; q < NP; q++) {
+      const uint32_t soff = part_off(q);
+#pragma unroll
+      for (int b = 0; b < kB; b++) x[q][b] = load_partial(part, (uint32_t)lane * 16 + (b0 + b) * 1024, soff);
+    }
+#pragma unroll
+    for (int b = 0; b < kB; b++) {
+      const uint4v own = __builtin_bit_cast(uint4v, acc[(b0 + b) >> 1][(b0 + b) & 1]);
+      float4v t;
+#pragma unroll
+      for (int q = 0; q < NP; q++) {
+        // Piece q's term: the own registers where q == p, chosen by a bit
+        // mask (kept opaque, so no branch replaces it).
+        uint32_t own_mask = q == p ? ~0u : 0u;
+        asm volatile("" : "+v"(own_mask));
+        const float4v term =
+            __builtin_bit_cast(float4v, (__builtin_bit_cast(uint4v, x[q][b]) & ~own_mask) | (own & own_mask));
+        t = q == 0 ? term : t + term;
+      }
+      acc[(b0 + b) >> 1][(b0 + b) & 1] = t;
+    }
+  }
+}
+
+template <typename PartOff>
+__device__ __forceinline__ void split_sum(float4v (&acc)[4][2], int np, int p, int lane,
+                                          __amdgpu_buffer_rsrc_t part, PartOff part_off) {
+  // The counter read that made this wave the last stays before these reads.
+  asm volatile("" ::: "memory");
+  static_assert(kFillMaxPieces == 8, "one case per piece count");
+  switch (np) {
+    case 2: split_sum_n<2>(acc, p, lane, part, part_off); break;
+    case 3: split_sum_n<3>(acc, p, lane, part, part_off); break;
+    case 4: split_sum_n<4>(acc, p, lane, part, part_off); break;
+    case 5: split_sum_n<5>(acc, p, lane, part, part_off); break;
+    case 6: split_sum_n<6>(acc, p, lane, part, part_off); break;
+    case 7: split_sum_n<7>(acc, p, lane, part, part_off); break;
+    default: split_sum_n<8>(acc, p, lane, part, part_off); break;
+  }
+}
+
+// kSplit: this workgroup is unit blockIdx.x of the split plan {0, units,
+// pieces, chunks}; part and counters are the workspace.
+template <typename OutT, bool kEdge, bool kSplit>
 __global__ __launch_bounds__(kThreads) void f16_pp128_kernel(const half_t* __restrict__ A,
                                                              const half_t* __restrict__ B,
-                                                             OutT* __restrict__ C, int M, int N, int K) {
+                                                             OutT* __restrict__ C, int M, int N, int K, int units,
+                                                             int pieces, int chunks, float* __restrict__ part,
+                                                             unsigned* __restrict__ counters) {
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int grp = wave >> 2;  // 0 = P, 1 = Q; waves w and w+4 share a SIMD
   const int gw = wave & 3;
   constexpr int kR = kEdge ? 1 : 0;  // round the tile and k-tile counts up
-  int tm, tn;
-  tile_of(blockIdx.x, (M + kR * (kBM - 1)) / kBM, (N + kR * (kBN - 1)) / kBN, tm, tn);
+  const int tiles_m = (M + kR * (kBM - 1)) / kBM, tiles_n = (N + kR * (kBN - 1)) / kBN;
+  const int iters = (K + kR * (kBK - 1)) / kBK;
+  int tm, tn, kb = 0, nk = iters;
+  SkWork w{};
+  if constexpr (kSplit) {
+    w = sk_work(blockIdx.x, tiles_m * tiles_n, iters, SkPlan{0, units, pieces, chunks}, kFillLastExtra);
+    raster_tile(w.cid, tiles_m, tiles_n, tm, tn);
+    kb = w.kb;
+    nk = w.ke - w.kb;
+  } else {
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  }
   const int m0 = tm * kBM, n0 = tn * kBN;
-  const int nk = (K + kR * (kBK - 1)) / kBK;
   const uint32_t lds_base = lds_addr32(lds);
 
   // ---- direct-to-LDS duty: instruction d = 4h + i (8 per wave per k-tile) ----
@@ -179,9 +288,10 @@ __global__ __launch_bounds__(kThreads) void f16_pp128_kernel(const half_t* __res
       voff[i] = (uint32_t)(((size_t)krow * N + c * 8) * 2);
     }
   }
-  const char* g_base = grp ? reinterpret_cast<const char*>(A) + (size_t)m0 * K * 2
-                           : reinterpret_cast<const char*>(B) + (size_t)n0 * 2;
-  const size_t g_kt = grp ? (size_t)kBK * 2 : (size_t)kBK * N * 2;   // per k-tile
+  const size_t g_kt = grp ? (size_t)kBK * 2 : (size_t)kBK * N * 2;  // per k-tile
+  const char* g_base = (grp ? reinterpret_cast<const char*>(A) + (size_t)m0 * K * 2
+                            : reinterpret_cast<const char*>(B) + (size_t)n0 * 2) +
+                       (size_t)kb * g_kt;  // k-tile kb: local k-tile 0
   const size_t g_h = grp ? (size_t)64 * K * 2 : (size_t)16 * N * 2;  // per h
   const uint32_t l_base = lds_base + (grp ? (uint32_t)kATop + gw * 16 * kRowBytes : (uint32_t)kBOff + gw * 32 * kBRowBytes);
   const uint32_t l_slot = grp ? (uint32_t)kHalfBytes : (uint32_t)kBBytes;  // per slot
@@ -230,7 +340,7 @@ __global__ __launch_bounds__(kThreads) void f16_pp128_kernel(const half_t* __res
 #pragma unroll
       for (int i = 0; i < 4; i++) o.l[4 * h + i] = ls + h * l_h + i * 1024;
     }
-    o.kleft = kEdge && grp ? (uint32_t)(K - kt * kBK) : (uint32_t)kBK;
+    o.kleft = kEdge && grp ? (uint32_t)(K - (kb + kt) * kBK) : (uint32_t)kBK;
     return o;
   };
   auto pin_ops = [&](const DmaOps& o) {
@@ -358,6 +468,20 @@ __global__ __launch_bounds__(kThreads) void f16_pp128_kernel(const half_t* __res
   wait_vmcnt<0>();
   lds_barrier();
 
+  unsigned* cnt = nullptr;
+  if constexpr (kSplit) {
+    const __amdgpu_buffer_rsrc_t prsrc =
+        __builtin_amdgcn_make_buffer_rsrc(part, 0, (int)((size_t)units * kSlotBytes), kBufferWord3);
+    const SkPlan plan{0, units, pieces, chunks};
+    auto part_off = [&](int q) {
+      return (uint32_t)((size_t)sk_unit_of(plan, tiles_m * tiles_n, w.tile, q) * kSlotBytes) +
+             (uint32_t)wave * kWaveSlotBytes;
+    };
+    cnt = counters + (size_t)w.tile * kSkWaves + wave;
+    if (!split_arrive(acc, w.np, w.p, lane, prsrc, part_off, cnt)) return;
+    split_sum(acc, w.np, w.p, lane, prsrc, part_off);
+  }
+
   // ---- epilogue: the ring is idle; each wave stages its block in its own region ----
   const uint32_t wstage = lds_base + wave * Epi<OutT>::kRegion;
 #pragma unroll
@@ -369,26 +493,55 @@ __global__ __launch_bounds__(kThreads) void f16_pp128_kernel(const half_t* __res
     Epi<OutT>::store_edge(wstage, C, M, N, m0 + grp * 64, n0 + gw * 32, lane);
   else
     Epi<OutT>::store(wstage, C + (size_t)(m0 + grp * 64) * N + n0 + gw * 32, N, lane);
+  if constexpr (kSplit) {
+    if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 }
 
-template <typename OutT, bool kEdge>
-hipError_t launch_t(const GemmArgs& a) {
+// The split plan of a shape (tiles and k-tiles rounded up).
+SkPlan plan_of(size_t m, size_t n, size_t k, int num_cus) {
+  const int64_t tiles = (int64_t)(((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN));
+  return sk_plan_fill(tiles, (int64_t)((k + kBK - 1) / kBK), num_cus);
+}
+
+size_t workspace(size_t m, size_t n, size_t k, int num_cus) {
+  const SkPlan p = plan_of(m, n, k, num_cus);
+  return p.units ? kSkCounterBytes + (size_t)p.units * kSlotBytes : 0;
+}
+
+template <typename OutT, bool kEdge, bool kSplit>
+hipError_t launch_t(const GemmArgs& a, const SkPlan& p) {
   static std::atomic<uint64_t> attr_done{0};
-  auto kfn = f16_pp128_kernel<OutT, kEdge>;
+  auto kfn = f16_pp128_kernel<OutT, kEdge, kSplit>;
   hipError_t e = ensure_lds_attr(kfn, kLdsBytes, a.device, attr_done);
   if (e != hipSuccess) return e;
-  const size_t r = kEdge ? 1 : 0;
-  const int tiles = (int)(((a.m + r * (kBM - 1)) / kBM) * ((a.n + r * (kBN - 1)) / kBN));
-  hipLaunchKernelGGL(kfn, dim3(tiles), dim3(kThreads), kLdsBytes, a.stream, static_cast<const half_t*>(a.A),
-                     static_cast<const half_t*>(a.B), static_cast<OutT*>(a.C), (int)a.m, (int)a.n, (int)a.k);
+  unsigned* counters = nullptr;
+  float* part = nullptr;
+  if constexpr (kSplit) {
+    counters = static_cast<unsigned*>(a.workspace);
+    part = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + kSkCounterBytes);
+    if (!a.workspace_clean) {
+      e = zero_words(counters, kSkCounterBytes / sizeof(unsigned), a.stream);
+      if (e != hipSuccess) return e;
+    }
+  }
+  hipLaunchKernelGGL(kfn, dim3((unsigned)(kSplit ? p.units : p.dp)), dim3(kThreads), kLdsBytes, a.stream,
+                     static_cast<const half_t*>(a.A), static_cast<const half_t*>(a.B), static_cast<OutT*>(a.C),
+                     (int)a.m, (int)a.n, (int)a.k, p.units, p.pieces, p.chunks, part, counters);
   return hipGetLastError();
+}
+
+template <typename OutT>
+hipError_t launch_out(const GemmArgs& a) {
+  const SkPlan p = plan_of(a.m, a.n, a.k, a.num_cus);
+  const bool grid = a.m % kBM == 0 && a.n % kBN == 0 && a.k % kBK == 0;
+  if (p.units > 0) return grid ? launch_t<OutT, false, true>(a, p) : launch_t<OutT, true, true>(a, p);
+  return grid ? launch_t<OutT, false, false>(a, p) : launch_t<OutT, true, false>(a, p);
 }
 
 // Shapes on the 128 x 128 x 128 grid run without the edge treatment.
 hipError_t launch(const GemmArgs& a) {
-  const bool grid = a.m % kBM == 0 && a.n % kBN == 0 && a.k % kBK == 0;
-  if (a.out_dtype == VK_DTYPE_F16) return grid ? launch_t<half_t, false>(a) : launch_t<half_t, true>(a);
-  return grid ? launch_t<float, false>(a) : launch_t<float, true>(a);
+  return a.out_dtype == VK_DTYPE_F16 ? launch_out<half_t>(a) : launch_out<float>(a);
 }
 
 // 32-bit lane offsets (64 rows of A, 128 k-rows of B past the scalar base),
@@ -411,8 +564,9 @@ void register_f16_pp128() {
   e.name = "f16_v11_pp128_bk128";
   e.caps = make_caps(11, VK_DTYPE_F16, kOutF16 | kOutF32, 1, 8, 8, 16, pp128::kBM,
                      pp128::kBN, pp128::kBK, pp128::kThreads, pp128::kLdsBytes, 0, 0);
+  e.caps.uses_workspace = 1;
   e.launch = pp128::launch;
-  e.workspace = nullptr;
+  e.workspace = pp128::workspace;
   e.shape_ok = pp128::shape_ok;
   register_kernel(e);
 }

@@ -1,6 +1,7 @@
 // vk_splittail.hpp -- the tail schedule of the 256x256-tile fp16 GEMM
-// (version 9): which workgroup computes which k-range of which tile, and
-// where the pieces of a split tile meet.  Host and device code share these
+// (version 9) and the split of under-filled 128x128-tile grids (version 11):
+// which workgroup computes which k-range of which tile, and where the pieces
+// of a split tile meet.  Host and device code share these
 // functions, so the launch, the kernel and the schedule's own tests agree.
 //
 // With T tiles of I k-tile iterations each on C compute units (one workgroup
@@ -49,8 +50,8 @@ struct SkPlan {
 // partials while it computes, so that when it finishes it usually finds them
 // all in memory (the counter already at s - 1) and skips writing its own.
 constexpr int kSkLastExtra = 3;
-__host__ __device__ inline int sk_piece_begin(int p, int I, int s) {
-  return (int)((int64_t)p * (I - kSkLastExtra) / s);
+__host__ __device__ inline int sk_piece_begin(int p, int I, int s, int extra = kSkLastExtra) {
+  return (int)((int64_t)p * (I - extra) / s);
 }
 
 // Cost model of the tail, in thousandths of a k-tile iteration of a full
@@ -94,6 +95,28 @@ __host__ __device__ inline SkPlan sk_plan(int64_t T, int64_t I, int num_cus) {
   return SkPlan{(int)dp, (int)(best * r), (int)best, chunks};
 }
 
+// Version 11 (128x128 tiles) splits whole grids that fill at most half of the
+// CUs: T tiles of I k-tiles on C CUs with 2T <= C, every tile cut into
+// s = min(8, C / T, I / 8) pieces (no whole tiles: dp = 0), the last piece
+// kFillLastExtra k-tiles longer.  With T % 8 == 0 each XCD takes the pieces
+// of its own share of the raster.  A piece of fewer than 8 k-tiles (~1 us
+// each) does not repay the hand-off, measured on MI355X at 3-6 us (a piece's
+// partial published in 1.4-3.2 us, the last arrival's reads 1.2-4.5 us):
+// 1000^3 (8 k-tiles) took 12.8 us in 2 pieces against 9.8 whole.
+constexpr int kFillMinIters = 8;
+constexpr int kFillMaxPieces = 8;
+constexpr int kFillLastExtra = 1;
+__host__ __device__ inline SkPlan sk_plan_fill(int64_t T, int64_t I, int num_cus) {
+  const SkPlan whole{(int)T, 0, 1, 1};
+  const int64_t C = num_cus < kSkMaxUnits ? num_cus : kSkMaxUnits;
+  if (C <= 0 || T <= 0 || 2 * T > C) return whole;
+  int64_t s = C / T;
+  if (s > kFillMaxPieces) s = kFillMaxPieces;
+  if (s > I / kFillMinIters) s = I / kFillMinIters;
+  if (s < 2) return whole;
+  return SkPlan{0, (int)(s * T), (int)s, T % 8 == 0 ? 8 : 1};
+}
+
 // The work of one workgroup: k-tile iterations [kb, ke) of the tile at raster
 // position cid, which is piece p of np.  For a split tile, `tile` numbers it
 // among the tail tiles (for its counters) and the pieces of tile t are the
@@ -112,7 +135,7 @@ __host__ __device__ inline int sk_unit_of(const SkPlan& pl, int T, int tile, int
   return x + pl.chunks * (sl * pl.pieces + q);
 }
 
-__host__ __device__ inline SkWork sk_work(int bid, int T, int I, const SkPlan& pl) {
+__host__ __device__ inline SkWork sk_work(int bid, int T, int I, const SkPlan& pl, int extra = kSkLastExtra) {
   SkWork w{};
   if (bid < pl.dp) {
     w.cid = xcd_remap(bid, T);
@@ -131,8 +154,8 @@ __host__ __device__ inline SkWork sk_work(int bid, int T, int I, const SkPlan& p
   w.np = pl.pieces;
   w.tile = x * rc + sl;
   w.cid = (pl.chunks == 8 ? x * (T >> 3) + (pl.dp >> 3) : pl.dp) + sl;
-  w.kb = sk_piece_begin(w.p, I, pl.pieces);
-  w.ke = w.p + 1 < pl.pieces ? sk_piece_begin(w.p + 1, I, pl.pieces) : I;
+  w.kb = sk_piece_begin(w.p, I, pl.pieces, extra);
+  w.ke = w.p + 1 < pl.pieces ? sk_piece_begin(w.p + 1, I, pl.pieces, extra) : I;
   return w;
 }
 

@@ -117,16 +117,18 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
     (fastest first; version 10 takes shapes off the 256 x 256 x 64 grid
     whose N and K are multiples of 8), then the any-shape kernel.  Version 11
     is taken, with T its 128 x 128 tiles on C compute units:
-      * on the 256 x 256 x 64 grid, where T <= C and either 4 T > C or the
-        split-tail plan of version 9 splits nothing (measured on MI355X:
-        1024 x 4096 x 4096 33.6 us against 46.2 for version 9 and 64.5 for
-        version 7; 1024 x 1024 x 8192, T = 64, 47.3 against version 9's
-        43.9; 1536 x 4096 x 4096, T = 384, 58.7 against 50.6);
+      * on the 256 x 256 x 64 grid, where T <= C (one wave; with 2 T <= C it
+        splits K over the idle CUs itself).  Measured on MI355X, us per
+        launch against version 9's split tail: 1024 x 4096 x 4096 33.6
+        against 46.2 (version 7: 64.5), 1024 x 1024 x 8192 29.1 against
+        43.9, 512 x 512 x 8192 19.7 against 41.7, 512 x 4096 x 4096 24.7
+        against 35.1; beyond one wave 1536 x 4096 x 4096 (T = 384) took 58.7
+        against 50.6;
       * off it, where T <= 3 C / 2 (version 10, whose split pieces do not stay
         on one XCD there and whose edge tiles are twice as wide, measured
         slower on every such shape: 1000 x 1000 x 1000 23.0 us against 9.8,
         2000 x 3000 x 1000 (T = 384) 25.2 against 21.2, 1000 x 1000 x 4000
-        (T = 64) 36.7 against 29.2).
+        (T = 64) 36.6 against 23.0).
     The split-tail version 9 comes first among the 256x256 kernels only where
     its schedule splits tiles on this device (it then needs a workspace);
     elsewhere it would run version 7's whole tiles.  The reference picks
@@ -146,8 +148,7 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
             cus = cus or _num_cus()
             tiles = -(-m // 128) * -(-n // 128)
             if m % 256 == 0 and n % 256 == 0 and k % 64 == 0:
-                splits = 9 in avail and _abi.workspace_bytes(9, in_dt, m, n, k) > 0
-                if not (tiles <= cus and (4 * tiles > cus or not splits)):
+                if tiles > cus:
                     continue
             elif 2 * tiles > 3 * cus:
                 continue
