@@ -139,7 +139,10 @@ def test_pick_version_follows_shape():
     assert vk.pick_version(128, 8192, 8192) == 8  # batch-128 decode: still the split-K kernel
     assert vk.pick_version(144, 8192, 8192) == 8  # 2 x 2 waves up to 256 rows
     assert vk.pick_version(1, 8192, 8192) == 8    # one row: the same kernel, rows past M read as zeros
-    assert vk.pick_version(256, 8192, 8192) == 8
+    assert vk.pick_version(256, 8192, 8192) == 11  # from 192 rows: 128 x 128 tiles, K split over idle CUs
+    assert vk.pick_version(192, 4096, 4096) == 11
+    assert vk.pick_version(160, 4096, 4096) == 8
+    assert vk.pick_version(192, 28672, 8192) == 8  # 448 tiles of 128 x 128 off the grid: over 1.5 waves
     assert vk.pick_version(300, 8192, 8192) == 11  # beyond 256 rows, off the grid: 192 tiles of 128 x 128
     assert vk.pick_version(4096, 4096, 4096) == 7  # 256 tiles: one full wave
     assert vk.pick_version(4096, 4096, 4096, "f16", "f32") == 7

@@ -1,6 +1,7 @@
-"""Stream capture (HIP graphs) of the C ABI: a split-tail call (version 10 on
-1000 x 1000 x 4000, whose tail tiles are cut into pieces that meet through a
-workspace) captured with a caller workspace (vk_gemm_ws) and replayed several
+"""Stream capture (HIP graphs) of the C ABI: a split call on 1000 x 1000 x
+4000 (version 10, whose tail tiles are cut into pieces that meet through a
+workspace, and version 11, whose 64 tiles of 128 x 128 are each cut into 4
+k-slices) captured with a caller workspace (vk_gemm_ws) and replayed several
 times, with eager work and synchronisations between the replays, each replay
 bit-identical to the eager call and within the fp32 bound of the exact
 product; the same call through the library workspace (vk_gemm) is refused
@@ -18,20 +19,21 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
-def test_split_tail_capture_and_replay(gpu, oracle):
+@pytest.mark.parametrize("version", [10, 11])
+def test_split_tail_capture_and_replay(gpu, oracle, version):
     import torch
     import vibekernel_amd as vk
     from vibekernel_amd import _abi
     m, n, k = 1000, 1000, 4000
     A, B = make_inputs(m, n, k, "uniform", seed=31)
     tA, tB = torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda()
-    need = _abi.workspace_bytes(10, vk.DTYPE_F16, m, n, k)
-    assert need > 0  # the plan splits this shape's tail
+    need = _abi.workspace_bytes(version, vk.DTYPE_F16, m, n, k)
+    assert need > 0  # the plan splits this shape
     ws = torch.empty(need, dtype=torch.uint8, device="cuda:0")
     C_eager = torch.full((m, n), float("nan"), dtype=torch.float16, device="cuda:0")
-    announce("capture: eager v10 1000x1000x4000 with caller workspace")
+    announce(f"capture: eager v{version} 1000x1000x4000 with caller workspace")
     s = torch.cuda.current_stream()
-    st = _abi.gemm_ws(10, vk.DTYPE_F16, vk.DTYPE_F16, m, n, k, _ptr(tA), _ptr(tB), _ptr(C_eager),
+    st = _abi.gemm_ws(version, vk.DTYPE_F16, vk.DTYPE_F16, m, n, k, _ptr(tA), _ptr(tB), _ptr(C_eager),
                       _ptr(ws), need, _ptr_stream(s))
     assert st == 0
     torch.cuda.synchronize()
@@ -46,9 +48,9 @@ def test_split_tail_capture_and_replay(gpu, oracle):
         with torch.cuda.graph(g, stream=side):
             cs = torch.cuda.current_stream()
             # the library workspace is refused under capture
-            st_lib = _abi.gemm(10, vk.DTYPE_F16, vk.DTYPE_F16, m, n, k, _ptr(tA), _ptr(tB), _ptr(C),
+            st_lib = _abi.gemm(version, vk.DTYPE_F16, vk.DTYPE_F16, m, n, k, _ptr(tA), _ptr(tB), _ptr(C),
                                _ptr_stream(cs))
-            st_ws = _abi.gemm_ws(10, vk.DTYPE_F16, vk.DTYPE_F16, m, n, k, _ptr(tA), _ptr(tB), _ptr(C),
+            st_ws = _abi.gemm_ws(version, vk.DTYPE_F16, vk.DTYPE_F16, m, n, k, _ptr(tA), _ptr(tB), _ptr(C),
                                  _ptr(ws), need, _ptr_stream(cs))
     torch.cuda.current_stream().wait_stream(side)
     assert st_lib == -6 and st_ws == 0
@@ -56,7 +58,7 @@ def test_split_tail_capture_and_replay(gpu, oracle):
         C.fill_(float("nan"))
         torch.matmul(tA[:64].float(), tB[:, :64].float())  # eager work between replays
         torch.cuda.synchronize()
-        announce(f"capture: replay {r}")
+        announce(f"capture: v{version} replay {r}")
         g.replay()
         torch.cuda.synchronize()
         assert np.array_equal(C.cpu().numpy().view(np.uint16), ref.view(np.uint16)), f"replay {r}"

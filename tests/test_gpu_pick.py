@@ -11,7 +11,8 @@ pytestmark = pytest.mark.gpu
 
 F16_CASES = [
     ((1, 256, 64), 8),           # one row: the skinny split-K kernel
-    ((200, 1024, 2048), 8),      # 2 x 2 waves
+    ((160, 1024, 2048), 8),      # 2 x 2 waves
+    ((200, 1024, 2048), 11),     # from 192 rows: 128 x 128 tiles (off the grid, K split)
     ((16, 8224, 256), 8),        # n % 128 != 0: the last column block cut short
     ((4096, 4096, 256), 7),      # one full wave of 256 x 256 tiles
     ((512, 512, 512), 11),       # 16 tiles of 128 x 128 where 256 x 256 gives 4 (and no split)

@@ -112,8 +112,8 @@ def _num_cus() -> int:
 def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = None) -> int:
     """The fastest version that accepts this shape (checked with vk_gemm_check
     on 4 KiB-aligned placeholder addresses; nothing is launched): for fp16
-    the skinny kernels when M <= 256 (64 for version 4), then the 128 x 128
-    tiles of version 11 where they suit the grid, then the 256x256 kernels
+    the skinny kernels when M < 192 (version 8; version 4 up to 64), then the
+    128 x 128 tiles of version 11 where they suit the grid, then the 256x256 kernels
     (fastest first; version 10 takes shapes off the 256 x 256 x 64 grid
     whose N and K are multiples of 8), then the any-shape kernel.  Version 11
     is taken, with T its 128 x 128 tiles on C compute units:
@@ -129,6 +129,13 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
         slower on every such shape: 1000 x 1000 x 1000 23.0 us against 9.8,
         2000 x 3000 x 1000 (T = 384) 25.2 against 21.2, 1000 x 1000 x 4000
         (T = 64) 36.6 against 23.0).
+    From M = 192 to 256 version 11 also beats the skinny split-K version 8
+    wherever it is taken (us per launch, one box: 192 x 4096 x 4096 22.5
+    against 30.2, 192 x 8192 x 8192 39.8 against 46.0, 192 x 14336 x 4096
+    32.9 against 42.4, 256 x 8192 x 8192 39.8 against 55.6); below 192 rows
+    the two trade places with N and K (M = 128: 128 x 4096 x 4096 18.5
+    against 21.7, 128 x 4096 x 14336 39.1 against 34.4), and version 8 keeps
+    them.
     The split-tail version 9 comes first among the 256x256 kernels only where
     its schedule splits tiles on this device (it then needs a workspace);
     elsewhere it would run version 7's whole tiles.  The reference picks
@@ -138,19 +145,25 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
     out_dt = DTYPE_F16 if (out or dtype) == "f16" else DTYPE_F32
     order = [8, 4, 11, 9, 7, 10, 6, 5, 3, 2, 1] if in_dt == DTYPE_F16 else [2, 3, 1]
     avail = set(_abi.versions(in_dt))
-    cus = None
+
+    def takes(v):
+        return v in avail and _abi.check(v, in_dt, out_dt, m, n, k, 4096, 4096, 4096) == _abi.VK_OK
+
+    def v11_suits():
+        cus = _num_cus()
+        tiles = -(-m // 128) * -(-n // 128)
+        if m % 256 == 0 and n % 256 == 0 and k % 64 == 0:
+            return tiles <= cus
+        return 2 * tiles <= 3 * cus
+
     for v in order:
         if v not in avail:
             continue
+        if v == 8 and m >= 192 and in_dt == DTYPE_F16 and v11_suits() and takes(11):
+            continue
         if v == 9 and _abi.workspace_bytes(v, in_dt, m, n, k) == 0:
             continue
-        if v == 11:
-            cus = cus or _num_cus()
-            tiles = -(-m // 128) * -(-n // 128)
-            if m % 256 == 0 and n % 256 == 0 and k % 64 == 0:
-                if tiles > cus:
-                    continue
-            elif 2 * tiles > 3 * cus:
-                continue
-        if _abi.check(v, in_dt, out_dt, m, n, k, 4096, 4096, 4096) == _abi.VK_OK:
+        if v == 11 and not v11_suits():
+            continue
+        if takes(v):
             return v
