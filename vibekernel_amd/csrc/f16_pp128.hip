@@ -554,6 +554,344 @@ bool shape_ok(size_t m, size_t n, size_t k) {
          ((m + kBM - 1) / kBM) * ((n + kBN - 1) / kBN) < (1ull << 31);
 }
 
+// ---------------------------------------------------------------------------
+// Version 12: version 11's 128 x 128 tiles with 64 x 64 wave tiles.  In
+// version 11 each wave computes a 64 x 32 block over every k-tile and reads
+// 768 bytes of LDS fragments per MFMA; here each group of 4 waves takes
+// alternate 64-deep k-tiles of the whole tile (P the even ones, Q the odd
+// ones), each wave a 64 x 64 block (16 accumulators of 16 x 16), 512 bytes of
+// fragments per MFMA, and the two groups' sums are added at the end.
+//  * LDS ring: 5 slots of one k-tile (A 128 rows x 64 k, rows of 128 B with
+//    chunk ^ (row / 2) % 8; B 64 k-rows x 128 columns, rows of 256 B with
+//    version 11's transpose-read swizzle), 160 KB;
+//  * phase p (one barrier each): group p % 2 computes k-tile p from
+//    registers (32 MFMAs, each accumulator's 2 k-steps back to back) and
+//    issues the 8 loads per wave of k-tile p + 5 into slot p % 5, which
+//    k-tile p left; the other group reads k-tile p + 1's fragments and then
+//    waits until its own loads of k-tile p + 2 (issued 2 of its compute
+//    phases ago) have landed (vmcnt 8); each wave runs this as one loop over
+//    its own k-tiles, memory phase then compute phase;
+//  * afterwards P gives Q the right half of its block and Q gives P the left
+//    half (through LDS), so each wave holds a 64 x 32 block of P + Q (the
+//    sum of the even and of the odd k-tiles: fp32 addition commutes, so both
+//    halves are the same sum) -- version 11's block shape, whose epilogue and
+//    split hand-off are reused.
+// Results differ from version 11's in the order of the k-sum (two chains
+// added at the end) and are deterministic.  The split plan is version 11's,
+// over 128-deep k-units, each piece taking the 64-deep k-tiles of its units.
+namespace pp128w {
+
+constexpr int kBK = 64;                             // k-tile
+constexpr int kARow = kBK * 2;                      // 128 B: an A row of a k-tile
+constexpr int kABytes = kBM * kARow;                // 16 KB
+constexpr int kBRow = kBN * 2;                      // 256 B: a B k-row
+constexpr int kSlot = kABytes + kBK * kBRow;        // 32 KB
+constexpr int kSlots = 5;
+constexpr int kLdsBytes = kSlots * kSlot;           // 160 KB
+constexpr int kXchg = 64 * 1024;                    // the end's exchange regions: 8 x 8 KB
+static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
+static_assert(kXchg + 8 * 8192 <= kLdsBytes && 8 * Epi<float>::kRegion <= kXchg, "epilogue regions");
+
+__host__ __device__ constexpr int swz_a8(int row) { return (row >> 1) & 7; }
+
+template <typename OutT, bool kEdge, bool kSplit>
+__global__ __launch_bounds__(kThreads) void f16_pp128w_kernel(const half_t* __restrict__ A,
+                                                              const half_t* __restrict__ B,
+                                                              OutT* __restrict__ C, int M, int N, int K, int units,
+                                                              int pieces, int chunks, float* __restrict__ part,
+                                                              unsigned* __restrict__ counters) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;  // 0 = P (even k-tiles), 1 = Q (odd); waves w and w+4 share a SIMD
+  const int gw = wave & 3;
+  const int wr = gw >> 1, wc = gw & 1;  // the wave's 64 x 64 block of the tile
+  constexpr int kR = kEdge ? 1 : 0;
+  const int tiles_m = (M + kR * (kBM - 1)) / kBM, tiles_n = (N + kR * (kBN - 1)) / kBN;
+  const int nk_all = (K + kR * (kBK - 1)) / kBK;
+  int tm, tn, kb = 0, nk = nk_all;
+  SkWork w{};
+  if constexpr (kSplit) {
+    w = sk_work(blockIdx.x, tiles_m * tiles_n, (nk_all + 1) / 2, SkPlan{0, units, pieces, chunks}, kFillLastExtra);
+    raster_tile(w.cid, tiles_m, tiles_n, tm, tn);
+    kb = 2 * w.kb;
+    nk = min(2 * w.ke, nk_all) - kb;
+  } else {
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  }
+  const int m0 = tm * kBM, n0 = tn * kBN;
+  const uint32_t lds_base = lds_addr32(lds);
+
+  // ---- direct-to-LDS duty: 8 loads per wave per k-tile, issued by the group computing ----
+  // A load i (0..3): rows 32 gw + 8 i + l / 8, lane l at chunk position l % 8,
+  //   which holds chunk (l % 8) ^ swz_a8(row).
+  // B load i (0..3): k-rows 16 gw + 4 i + l / 16, position l % 16, holding
+  //   chunk (l % 16) ^ swz_b(krow).
+  uint32_t voa[4], vob[4], akin = 0;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int row = gw * 32 + 8 * i + (lane >> 3);
+    const int ca = (lane & 7) ^ swz_a8(row);
+    voa[i] = (uint32_t)(((size_t)row * K + ca * 8) * 2);
+    akin |= (uint32_t)(ca * 8) << (8 * i);  // kEdge: the chunk's first k within the k-tile
+    const int krow = gw * 16 + 4 * i + (lane >> 4);
+    const int cb = (lane & 15) ^ swz_b(krow);
+    vob[i] = (uint32_t)(((size_t)krow * N + cb * 8) * 2);
+  }
+  const char* ga0 = reinterpret_cast<const char*>(A) + ((size_t)m0 * K + (size_t)kb * kBK) * 2;
+  const char* gb0 = reinterpret_cast<const char*>(B) + ((size_t)kb * kBK * N + n0) * 2;
+  const uint32_t a_size = kEdge ? (uint32_t)((size_t)M * K * 2) : 0u;
+  const uint32_t b_size = kEdge ? (uint32_t)((size_t)K * N * 2) : 0u;
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(A), 0, (int)a_size, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(B), 0, (int)b_size, kBufferWord3);
+  const uint32_t sa0 = (uint32_t)(ga0 - reinterpret_cast<const char*>(A));  // kEdge: below 2^31
+  const uint32_t sb0 = (uint32_t)(gb0 - reinterpret_cast<const char*>(B));
+  const uint32_t la0 = lds_base + (uint32_t)(gw * 32 * kARow);
+  const uint32_t lb0 = lds_base + (uint32_t)(kABytes + gw * 16 * kBRow);
+
+  struct Ops {
+    const char* ga;
+    const char* gb;
+    uint32_t sa, sb;   // kEdge: scalar offsets into the buffers
+    uint32_t kleft;    // kEdge: k from the k-tile's start to K
+    uint32_t la, lb;   // LDS destination of load 0 (A, B)
+  };
+  auto ops_of = [&](int kt, int slot) {
+    Ops o;
+    o.ga = ga0 + (size_t)kt * kBK * 2;
+    o.gb = gb0 + (size_t)kt * kBK * N * 2;
+    o.sa = sa0 + (uint32_t)kt * (uint32_t)(kBK * 2);
+    o.sb = sb0 + (uint32_t)kt * (uint32_t)(kBK * N * 2);
+    o.kleft = kEdge ? (uint32_t)(K - (kb + kt) * kBK) : (uint32_t)kBK;
+    o.la = la0 + (uint32_t)(slot * kSlot);
+    o.lb = lb0 + (uint32_t)(slot * kSlot);
+    return o;
+  };
+  auto pin = [&](const Ops& o) {
+    if constexpr (kEdge)
+      asm volatile("" ::"s"(o.sa), "s"(o.sb), "s"(o.kleft));
+    else
+      asm volatile("" ::"s"(o.ga), "s"(o.gb));
+    asm volatile("" ::"s"(o.la), "s"(o.lb));
+  };
+  // load d: A for d < 4, B for d >= 4
+  auto dma_with = [&](int d, const Ops& o) {
+    const int i = d & 3;
+    if (d < 4) {
+      if constexpr (kEdge) {
+        const uint32_t off = ((akin >> (8 * i)) & 255u) < o.kleft ? voa[i] : a_size;  // a_size: zeros
+        dma16_buf(ra, off, o.sa, o.la + i * 1024);
+      } else {
+        dma16(o.ga, voa[i], o.la + i * 1024);
+      }
+    } else {
+      if constexpr (kEdge)
+        dma16_buf(rb, vob[i], o.sb, o.lb + i * 1024);
+      else
+        dma16(o.gb, vob[i], o.lb + i * 1024);
+    }
+  };
+  auto dma_all = [&](int kt, int slot) {
+    const Ops o = ops_of(kt, slot);
+#pragma unroll
+    for (int d = 0; d < 8; d++) dma_with(d, o);
+  };
+
+  // ---- fragment addresses ----
+  // A block i (rows 64 wr + 16 i + l % 16), k-step s: chunk 4 s + l / 16,
+  // swizzled by the row's bits 1..3 (= those of l % 16).
+  const int arow = lane & 15;
+  uint32_t aoff[2];
+#pragma unroll
+  for (int s = 0; s < 2; s++)
+    aoff[s] = (uint32_t)((wr * 64 + arow) * kARow + 16 * ((4 * s + (lane >> 4)) ^ swz_a8(arow)));
+  // B block j (columns 64 wc + 16 j ..), k-step s, half h: lane 16 g + 4 jj + q
+  // names k-row 32 s + 8 g + 4 h + jj and the 8-byte half q % 2 of chunk
+  // 8 wc + 2 j + q / 2 (as version 11).
+  const int g = lane >> 4, jj = (lane >> 2) & 3, q = lane & 3;
+  const int krow0 = 8 * g + jj;
+  uint32_t boff[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) {
+    const int c = wc * 8 + 2 * j + (q >> 1);
+    boff[j] = (uint32_t)(kABytes + krow0 * kBRow + 16 * (c ^ swz_b(krow0)) + 8 * (q & 1));
+  }
+
+  float4v acc[4][4];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 4; j++) acc[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+  half8 fa[2][4], fb[2][4];  // [k-step][block]
+  auto read_frags = [&](int slot) {
+    const uint32_t sl = lds_base + (uint32_t)(slot * kSlot);
+    uint32_t va[2], vb[4];
+#pragma unroll
+    for (int s = 0; s < 2; s++) va[s] = sl + aoff[s];
+#pragma unroll
+    for (int j = 0; j < 4; j++) vb[j] = sl + boff[j];
+    static_for<2>([&](auto sc) {
+      constexpr int s = decltype(sc)::value;
+      static_for<4>([&](auto ic) {
+        constexpr int i = decltype(ic)::value;
+        fa[s][i] = lds_read_h8_off<i * 16 * kARow>(va[s]);
+      });
+#pragma unroll
+      for (int j = 0; j < 4; j++) {
+        const half4 lo = lds_read_tr16_off<s * 32 * kBRow>(vb[j]);
+        const half4 hi = lds_read_tr16_off<s * 32 * kBRow + 4 * kBRow>(vb[j]);
+        fb[s][j] = half8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+    });
+  };
+  // 32 MFMAs, each accumulator's 2 k-steps back to back, with the 8 loads of
+  // `o` interleaved (one after every second accumulator).
+  auto compute_and_load = [&](const Ops& o) {
+#pragma unroll
+    for (int x = 0; x < 16; x++) {
+      const int i = x >> 2, j = x & 3;
+      acc[i][j] = mfma16x16x32(fb[0][j], fa[0][i], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+      acc[i][j] = mfma16x16x32(fb[1][j], fa[1][i], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (x & 1) {
+        dma_with(x >> 1, o);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
+  };
+
+  // ---- prologue: k-tiles 0..4 (Q loads the even ones, P the odd ones) ----
+  // A k-tile past the last one is the last one again, into its own slot, so
+  // every compute phase issues 8 loads and the waits stay fixed.
+#pragma unroll
+  for (int j = 0; j < kSlots; j++)
+    if ((j & 1) != grp) dma_all(min(j, nk - 1), j);
+  if (grp) wait_vmcnt<16>();  // Q: k-tile 0
+  lds_barrier();
+  // Every wave runs the same loop over its own k-tiles j = grp, grp + 2, ...:
+  // a memory phase (phase j - 1: k-tile j's fragments, then the wait for this
+  // group's loads of k-tile j + 1, issued two of its compute phases ago) and
+  // a compute phase (phase j), one barrier after each.  Q starts one phase
+  // later (phase -1 idle), and a group that computes no k-tile in the last
+  // phase takes its barrier at the end, so every wave passes nk + 1 phase
+  // barriers.  The fragments go from the reads to the MFMAs of the same
+  // iteration, so they stay in their registers (their consumers come after
+  // the barrier's lgkmcnt(0)).
+  if (grp) lds_barrier();
+  int phases = grp;
+  for (int j = grp; j < nk; j += 2) {
+    __builtin_amdgcn_sched_barrier(0);
+    read_frags(j % kSlots);
+    __builtin_amdgcn_sched_barrier(0);
+    const Ops o = ops_of(min(j + kSlots, nk - 1), j % kSlots);
+    pin(o);
+    wait_vmcnt<8>();  // this group's loads of k-tile j + 1
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    __builtin_amdgcn_sched_barrier(0);
+    compute_and_load(o);
+    __builtin_amdgcn_sched_barrier(0);
+    lds_barrier();
+    phases += 2;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  if (phases < nk + 1) lds_barrier();
+  wait_vmcnt<0>();
+  lds_barrier();
+
+  // ---- P + Q: P keeps columns 0..31 of the block (j = 0, 1), Q columns 32..63 ----
+  {
+    const uint32_t give = lds_base + (uint32_t)(kXchg + wave * 8192);
+    const uint32_t take = lds_base + (uint32_t)(kXchg + (wave ^ 4) * 8192);
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) lds_write16(give + ((i * 2 + h) * 64 + lane) * 16, acc[i][grp ? h : 2 + h]);
+    lds_barrier();
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int h = 0; h < 2; h++) {
+        const float4v o = __builtin_bit_cast(float4v, lds_read16(take + ((i * 2 + h) * 64 + lane) * 16));
+        acc[i][h] = acc[i][grp ? 2 + h : h] + o;
+      }
+  }
+  float4v blk[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int h = 0; h < 2; h++) blk[i][h] = acc[i][h];
+  const int row0 = m0 + wr * 64, col0 = n0 + wc * 64 + grp * 32;
+
+  unsigned* cnt = nullptr;
+  if constexpr (kSplit) {
+    const __amdgpu_buffer_rsrc_t prsrc =
+        __builtin_amdgcn_make_buffer_rsrc(part, 0, (int)((size_t)units * kSlotBytes), kBufferWord3);
+    const SkPlan plan{0, units, pieces, chunks};
+    auto part_off = [&](int qq) {
+      return (uint32_t)((size_t)sk_unit_of(plan, tiles_m * tiles_n, w.tile, qq) * kSlotBytes) +
+             (uint32_t)wave * kWaveSlotBytes;
+    };
+    cnt = counters + (size_t)w.tile * kSkWaves + wave;
+    if (!split_arrive(blk, w.np, w.p, lane, prsrc, part_off, cnt)) return;
+    split_sum(blk, w.np, w.p, lane, prsrc, part_off);
+  }
+
+  // ---- epilogue: each wave stages its 64 x 32 block in its own region ----
+  const uint32_t wstage = lds_base + wave * Epi<OutT>::kRegion;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int h = 0; h < 2; h++) Epi<OutT>::stage(wstage, lane, i, h, blk[i][h]);
+  wait_lgkmcnt0();  // a wave reads back only its own region
+  if constexpr (kEdge)
+    Epi<OutT>::store_edge(wstage, C, M, N, row0, col0, lane);
+  else
+    Epi<OutT>::store(wstage, C + (size_t)row0 * N + col0, N, lane);
+  if constexpr (kSplit) {
+    if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+template <typename OutT, bool kEdge, bool kSplit>
+hipError_t launch_t(const GemmArgs& a, const SkPlan& p) {
+  static std::atomic<uint64_t> attr_done{0};
+  auto kfn = f16_pp128w_kernel<OutT, kEdge, kSplit>;
+  hipError_t e = ensure_lds_attr(kfn, kLdsBytes, a.device, attr_done);
+  if (e != hipSuccess) return e;
+  unsigned* counters = nullptr;
+  float* part = nullptr;
+  if constexpr (kSplit) {
+    counters = static_cast<unsigned*>(a.workspace);
+    part = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + kSkCounterBytes);
+    if (!a.workspace_clean) {
+      e = zero_words(counters, kSkCounterBytes / sizeof(unsigned), a.stream);
+      if (e != hipSuccess) return e;
+    }
+  }
+  hipLaunchKernelGGL(kfn, dim3((unsigned)(kSplit ? p.units : p.dp)), dim3(kThreads), kLdsBytes, a.stream,
+                     static_cast<const half_t*>(a.A), static_cast<const half_t*>(a.B), static_cast<OutT*>(a.C),
+                     (int)a.m, (int)a.n, (int)a.k, p.units, p.pieces, p.chunks, part, counters);
+  return hipGetLastError();
+}
+
+template <typename OutT>
+hipError_t launch_out(const GemmArgs& a) {
+  const SkPlan p = plan_of(a.m, a.n, a.k, a.num_cus);
+  const bool grid = a.m % kBM == 0 && a.n % kBN == 0 && a.k % kBK == 0;
+  if (p.units > 0) return grid ? launch_t<OutT, false, true>(a, p) : launch_t<OutT, true, true>(a, p);
+  return grid ? launch_t<OutT, false, false>(a, p) : launch_t<OutT, true, false>(a, p);
+}
+
+hipError_t launch(const GemmArgs& a) {
+  return a.out_dtype == VK_DTYPE_F16 ? launch_out<half_t>(a) : launch_out<float>(a);
+}
+
+}  // namespace pp128w
 }  // namespace pp128
 }  // namespace
 
@@ -569,6 +907,15 @@ void register_f16_pp128() {
   e.workspace = pp128::workspace;
   e.shape_ok = pp128::shape_ok;
   register_kernel(e);
+
+  KernelEntry e12 = e;
+  e12.version = 12;
+  e12.name = "f16_v12_pp128_k64alt";
+  e12.caps = make_caps(12, VK_DTYPE_F16, kOutF16 | kOutF32, 1, 8, 8, 16, pp128::kBM, pp128::kBN,
+                       pp128::pp128w::kBK, pp128::kThreads, pp128::pp128w::kLdsBytes, 0, 0);
+  e12.caps.uses_workspace = 1;
+  e12.launch = pp128::pp128w::launch;
+  register_kernel(e12);
 }
 
 }  // namespace vk
