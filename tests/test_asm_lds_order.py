@@ -1,6 +1,7 @@
-"""Device-assembly check of every HIP kernel in libvk_gemm.so (gfx950,
+"""Device-assembly checks of every HIP kernel in libvk_gemm.so (gfx950,
 compiled here with the library's flags to a temporary directory): no
-instruction reads a VGPR that an LDS read is still writing.
+instruction reads a VGPR that an LDS read is still writing, and every
+LDS-DMA load has its wait state after an M0 write.
 
 The fragment reads of the matrix-core kernels are inline asm
 (lds_read_h8_off / lds_read_tr16_off in vk_device.hpp), which the compiler
@@ -89,6 +90,30 @@ def scan(text):
     return out
 
 
+def m0_hazards(text):
+    """LDS-DMA loads (global_load_lds_*, buffer_load_* ... lds) issued right
+    after an SALU write of M0, which on the GFX9 family needs one wait state
+    between them (the kernels' inline asm puts an s_nop 0 there)."""
+    bad = []
+    prev = ""
+    for line in text.splitlines():
+        t = line.strip()
+        if not t or t[0] in ";." or t.endswith(":"):
+            continue
+        op = t.split()[0]
+        dma = op.startswith("global_load_lds") or (op.startswith("buffer_load") and t.endswith(" lds"))
+        if dma and prev.startswith("s_") and prev.split()[1:2] == ["m0,"]:
+            bad.append((prev, t))
+        prev = t
+    return bad
+
+
+def test_m0_scanner():
+    assert m0_hazards("\ts_mov_b32 m0, s4\n\tglobal_load_lds_dwordx4 v1, s[2:3]")
+    assert not m0_hazards("\ts_mov_b32 m0, s4\n\ts_nop 0\n\tglobal_load_lds_dwordx4 v1, s[2:3]")
+    assert m0_hazards("\ts_mov_b32 m0, s4\n\tbuffer_load_dwordx4 v1, s[4:7], s8 offen lds")
+
+
 def test_scanner_flags_a_read_before_the_wait():
     bad = """_Zk:
 \tds_read_b128 v[4:7], v1 offset:0
@@ -144,4 +169,9 @@ def test_no_kernel_reads_an_unretired_lds_result(device_asm):
             if hits:
                 found[f"{f}: {k}"] = hits[:3]
     assert kernels > 40  # every kernel instance of the library was scanned
+    assert not found, found
+
+
+def test_m0_wait_state_before_every_lds_dma(device_asm):
+    found = {f: m0_hazards(text)[:3] for f, text in device_asm.items() if m0_hazards(text)}
     assert not found, found
