@@ -35,7 +35,7 @@ def test_on_grid_equals_v7(gpu, shape, out):
                           C10.view(np.uint16 if out == "f16" else np.uint32))
 
 
-@pytest.mark.parametrize("version", [10, 11, 12])
+@pytest.mark.parametrize("version", [10, 11, 12, 13])
 @pytest.mark.parametrize("shape", [(300, 264, 72), (1, 8, 8), (257, 1000, 512), (600, 40, 1032), (257, 520, 4096)])
 @pytest.mark.parametrize("out", ["f16", "f32"])
 def test_writes_only_c(gpu, shape, out, version):
@@ -60,7 +60,7 @@ def test_writes_only_c(gpu, shape, out, version):
     assert np.array_equal(C.cpu().numpy().astype(np.int64), exact)
 
 
-@pytest.mark.parametrize("version", [10, 11, 12])
+@pytest.mark.parametrize("version", [10, 11, 12, 13])
 @pytest.mark.parametrize("out", ["f16", "f32"])
 def test_values_past_the_edges_never_reach_c(gpu, out, version):
     """M = 3, N = 8, K = 72: row 0's last k-tile covers k = 64..127, and
@@ -81,7 +81,7 @@ def test_values_past_the_edges_never_reach_c(gpu, out, version):
     assert np.array_equal(C[keep], exact[keep])
 
 
-@pytest.mark.parametrize("version", [10, 11, 12])
+@pytest.mark.parametrize("version", [10, 11, 12, 13])
 @pytest.mark.parametrize("shape", [(1000, 1000, 1000), (4096, 4096, 4128), (2000, 3000, 1000), (1000, 1000, 4000),
                                    (257, 520, 4096), (1496, 1496, 3000)])
 def test_ragged_random_vs_oracle(gpu, oracle, shape, version):
@@ -147,7 +147,7 @@ def test_split_caller_workspace(gpu):
         assert np.array_equal(tC.cpu().numpy(), ref)
 
 
-@pytest.mark.parametrize("version,dtype", [(10, "f16"), (11, "f16"), (12, "f16"), (3, "f32")])
+@pytest.mark.parametrize("version,dtype", [(10, "f16"), (11, "f16"), (12, "f16"), (13, "f16"), (3, "f32")])
 @pytest.mark.parametrize("shape", [(3, 8, 72), (17, 40, 200), (300, 264, 104), (100, 136, 2056)])
 def test_memory_past_the_operands_is_never_read(gpu, version, dtype, shape):
     """A and B are views at the start of larger buffers whose elements past

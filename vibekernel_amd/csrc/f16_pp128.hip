@@ -892,6 +892,319 @@ hipError_t launch(const GemmArgs& a) {
 }
 
 }  // namespace pp128w
+
+// ---------------------------------------------------------------------------
+// Version 13: version 11's tile and wave blocks (128 x 128 tiles, each wave a
+// 64 x 32 block over every k-tile) without the ping-pong.  In version 11 one
+// wave per SIMD reads fragments while the other computes, and a phase lasts
+// as long as that one wave needs to get its 24 KB of LDS reads through
+// (~820 cycles against ~580 of MFMA issue, measured): LDS serves a single
+// reading wave per SIMD at ~142 B/clk/CU, two at ~222.  Here every wave
+// computes its current 64-deep k-tile from registers while it reads the next
+// k-tile's fragments into a second register set (one LDS read after each
+// MFMA) and issues its 4 loads of the k-tile 4 ahead, so both waves of a SIMD
+// read and compute at once; one barrier per k-tile.
+//  * LDS ring: 5 slots of one k-tile, version 12's (A 128 rows x 64 k, rows
+//    of 128 B, chunk ^ (row / 2) % 8; B 64 k-rows x 128 columns, rows of
+//    256 B, version 11's transpose-read swizzle), 160 KB;
+//  * step t: compute k-tile t (fragments read during step t - 1), read
+//    k-tile t + 1's fragments, load k-tile t + 4 into slot (t + 4) % 5 (its
+//    previous k-tile, t - 1, was read during step t - 2); then wait for this
+//    wave's loads of k-tile t + 2 (vmcnt 8: the 4 loads of steps t - 1 and t
+//    may still fly) and barrier;
+//  * loads per step: wave w loads A rows 16 w .. 16 w + 15 (2 loads of 8
+//    rows) and B k-rows 8 w .. 8 w + 7 (2 loads of 4 k-rows);
+//  * each element is the same chain of MFMAs over 32-deep k-steps in
+//    ascending order as in versions 7 and 11 (bitwise equal where they run
+//    whole tiles).  Epilogue, edges and split hand-off are version 11's.
+namespace pp128n {
+
+using pp128w::kARow;
+using pp128w::kABytes;
+using pp128w::kBRow;
+using pp128w::kSlot;
+using pp128w::kSlots;
+using pp128w::swz_a8;
+constexpr int kBK = 64;
+constexpr int kLdsBytes = kSlots * kSlot;  // 160 KB
+
+template <typename OutT, bool kEdge, bool kSplit>
+__global__ __launch_bounds__(kThreads) void f16_pp128n_kernel(const half_t* __restrict__ A,
+                                                              const half_t* __restrict__ B,
+                                                              OutT* __restrict__ C, int M, int N, int K, int units,
+                                                              int pieces, int chunks, float* __restrict__ part,
+                                                              unsigned* __restrict__ counters) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;  // rows 64 grp .. 64 grp + 63 of the tile
+  const int gw = wave & 3;    // columns 32 gw .. 32 gw + 31
+  constexpr int kR = kEdge ? 1 : 0;
+  const int tiles_m = (M + kR * (kBM - 1)) / kBM, tiles_n = (N + kR * (kBN - 1)) / kBN;
+  const int nk_all = (K + kR * (kBK - 1)) / kBK;
+  int tm, tn, kb = 0, nk = nk_all;
+  SkWork w{};
+  if constexpr (kSplit) {
+    w = sk_work(blockIdx.x, tiles_m * tiles_n, (nk_all + 1) / 2, SkPlan{0, units, pieces, chunks}, kFillLastExtra);
+    raster_tile(w.cid, tiles_m, tiles_n, tm, tn);
+    kb = 2 * w.kb;
+    nk = min(2 * w.ke, nk_all) - kb;
+  } else {
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  }
+  const int m0 = tm * kBM, n0 = tn * kBN;
+  const uint32_t lds_base = lds_addr32(lds);
+
+  // ---- loads: 4 per wave per k-tile ----
+  // A load i (0, 1): rows 16 wave + 8 i + l / 8, lane l at chunk position
+  //   l % 8, holding chunk (l % 8) ^ swz_a8(row).
+  // B load i (0, 1): k-rows 8 wave + 4 i + l / 16, position l % 16, holding
+  //   chunk (l % 16) ^ swz_b(krow).
+  uint32_t voa[2], vob[2], akin = 0;
+#pragma unroll
+  for (int i = 0; i < 2; i++) {
+    const int row = wave * 16 + 8 * i + (lane >> 3);
+    const int ca = (lane & 7) ^ swz_a8(row);
+    voa[i] = (uint32_t)(((size_t)row * K + ca * 8) * 2);
+    akin |= (uint32_t)(ca * 8) << (8 * i);  // kEdge: the chunk's first k within the k-tile
+    const int krow = wave * 8 + 4 * i + (lane >> 4);
+    const int cb = (lane & 15) ^ swz_b(krow);
+    vob[i] = (uint32_t)(((size_t)krow * N + cb * 8) * 2);
+  }
+  const char* ga0 = reinterpret_cast<const char*>(A) + ((size_t)m0 * K + (size_t)kb * kBK) * 2;
+  const char* gb0 = reinterpret_cast<const char*>(B) + ((size_t)kb * kBK * N + n0) * 2;
+  const uint32_t a_size = kEdge ? (uint32_t)((size_t)M * K * 2) : 0u;
+  const uint32_t b_size = kEdge ? (uint32_t)((size_t)K * N * 2) : 0u;
+  const __amdgpu_buffer_rsrc_t ra =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(A), 0, (int)a_size, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rb =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<half_t*>(B), 0, (int)b_size, kBufferWord3);
+  const uint32_t sa0 = (uint32_t)(ga0 - reinterpret_cast<const char*>(A));  // kEdge: below 2^31
+  const uint32_t sb0 = (uint32_t)(gb0 - reinterpret_cast<const char*>(B));
+  const uint32_t la0 = lds_base + (uint32_t)(wave * 16 * kARow);
+  const uint32_t lb0 = lds_base + (uint32_t)(kABytes + wave * 8 * kBRow);
+
+  struct Ops {
+    const char* ga;
+    const char* gb;
+    uint32_t sa, sb, kleft, la, lb;
+  };
+  auto ops_of = [&](int kt, int slot) {
+    Ops o;
+    o.ga = ga0 + (size_t)kt * kBK * 2;
+    o.gb = gb0 + (size_t)kt * kBK * N * 2;
+    o.sa = sa0 + (uint32_t)kt * (uint32_t)(kBK * 2);
+    o.sb = sb0 + (uint32_t)kt * (uint32_t)(kBK * N * 2);
+    o.kleft = kEdge ? (uint32_t)(K - (kb + kt) * kBK) : (uint32_t)kBK;
+    o.la = la0 + (uint32_t)(slot * kSlot);
+    o.lb = lb0 + (uint32_t)(slot * kSlot);
+    return o;
+  };
+  auto pin = [&](const Ops& o) {
+    if constexpr (kEdge)
+      asm volatile("" ::"s"(o.sa), "s"(o.sb), "s"(o.kleft));
+    else
+      asm volatile("" ::"s"(o.ga), "s"(o.gb));
+    asm volatile("" ::"s"(o.la), "s"(o.lb));
+  };
+  // load d: A for d < 2, B for d >= 2
+  auto dma_with = [&](int d, const Ops& o) {
+    const int i = d & 1;
+    if (d < 2) {
+      if constexpr (kEdge) {
+        const uint32_t off = ((akin >> (8 * i)) & 255u) < o.kleft ? voa[i] : a_size;  // a_size: zeros
+        dma16_buf(ra, off, o.sa, o.la + i * 1024);
+      } else {
+        dma16(o.ga, voa[i], o.la + i * 1024);
+      }
+    } else {
+      if constexpr (kEdge)
+        dma16_buf(rb, vob[i], o.sb, o.lb + i * 1024);
+      else
+        dma16(o.gb, vob[i], o.lb + i * 1024);
+    }
+  };
+  auto dma_all = [&](int kt, int slot) {
+    const Ops o = ops_of(kt, slot);
+#pragma unroll
+    for (int d = 0; d < 4; d++) dma_with(d, o);
+  };
+
+  // ---- fragment addresses (version 12's A rows, version 11's B columns) ----
+  const int arow = lane & 15;
+  uint32_t aoff[2];
+#pragma unroll
+  for (int s = 0; s < 2; s++)
+    aoff[s] = (uint32_t)((grp * 64 + arow) * kARow + 16 * ((4 * s + (lane >> 4)) ^ swz_a8(arow)));
+  const int g = lane >> 4, jj = (lane >> 2) & 3, q = lane & 3;
+  const int krow0 = 8 * g + jj;
+  uint32_t boff[2];
+#pragma unroll
+  for (int j = 0; j < 2; j++) {
+    const int c = gw * 4 + 2 * j + (q >> 1);
+    boff[j] = (uint32_t)(kABytes + krow0 * kBRow + 16 * (c ^ swz_b(krow0)) + 8 * (q & 1));
+  }
+
+  float4v acc[4][2];
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) acc[i][j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // Fragments of one k-tile: A blocks i, B blocks j, k-steps s.
+  struct Frags {
+    half8 a[2][4], b[2][2];
+  };
+  // Read number r (0..15) of a k-tile's fragments: r < 8 the A read (s, i) =
+  // (r / 4, r % 4), then the B half-reads (s, j, h).
+  auto read_one = [&](Frags& f, uint32_t sl, auto rc) {
+    constexpr int r = decltype(rc)::value;
+    if constexpr (r < 8) {
+      constexpr int s = r / 4, i = r % 4;
+      f.a[s][i] = lds_read_h8_off<i * 16 * kARow>(sl + aoff[s]);
+    } else {
+      constexpr int s = (r - 8) / 4, j = ((r - 8) / 2) % 2, h = (r - 8) % 2;
+      const half4 v = lds_read_tr16_off<s * 32 * kBRow + h * 4 * kBRow>(sl + boff[j]);
+      if constexpr (h == 0) {
+        f.b[s][j][0] = v[0]; f.b[s][j][1] = v[1]; f.b[s][j][2] = v[2]; f.b[s][j][3] = v[3];
+      } else {
+        f.b[s][j][4] = v[0]; f.b[s][j][5] = v[1]; f.b[s][j][6] = v[2]; f.b[s][j][7] = v[3];
+      }
+    }
+  };
+  auto read_all = [&](Frags& f, int slot) {
+    const uint32_t sl = lds_base + (uint32_t)(slot * kSlot);
+    static_for<16>([&](auto rc) { read_one(f, sl, rc); });
+  };
+  // One step: the 16 MFMAs of `cur` (each accumulator's 2 k-steps back to
+  // back), after each one a read of `nxt` (when there is a next k-tile), and
+  // the 4 loads of `o` after every 4 MFMAs.
+  auto step = [&](const Frags& cur, Frags& nxt, int nslot, bool has_next, const Ops& o) {
+    const uint32_t sl = lds_base + (uint32_t)(nslot * kSlot);
+    static_for<8>([&](auto xc) {
+      constexpr int x = decltype(xc)::value;
+      constexpr int i = x >> 1, j = x & 1;
+      acc[i][j] = mfma16x16x32(cur.b[0][j], cur.a[0][i], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (has_next) read_one(nxt, sl, std::integral_constant<int, 2 * x>{});
+      __builtin_amdgcn_sched_barrier(0);
+      acc[i][j] = mfma16x16x32(cur.b[1][j], cur.a[1][i], acc[i][j]);
+      __builtin_amdgcn_sched_barrier(0);
+      if (has_next) read_one(nxt, sl, std::integral_constant<int, 2 * x + 1>{});
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (x & 1) {
+        dma_with(x >> 1, o);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    });
+  };
+
+  // ---- prologue: k-tiles 0..3 (a k-tile past the last one is the last one again) ----
+#pragma unroll
+  for (int j = 0; j < 4; j++) dma_all(min(j, nk - 1), j);
+  Frags f0, f1;
+  wait_vmcnt<12>();  // k-tile 0
+  lds_barrier();
+  read_all(f0, 0);
+  wait_vmcnt<8>();  // k-tile 1
+  lds_barrier();
+  // Steps in pairs, so the two fragment sets keep their registers.
+  int t = 0;
+  for (; t + 1 < nk; t += 2) {
+    {
+      const Ops o = ops_of(min(t + 4, nk - 1), (t + 4) % kSlots);
+      pin(o);
+      __builtin_amdgcn_sched_barrier(0);
+      step(f0, f1, (t + 1) % kSlots, true, o);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vmcnt<8>();  // this wave's loads of k-tile t + 2
+      lds_barrier();
+    }
+    {
+      const Ops o = ops_of(min(t + 5, nk - 1), (t + 5) % kSlots);
+      pin(o);
+      __builtin_amdgcn_sched_barrier(0);
+      step(f1, f0, (t + 2) % kSlots, t + 2 < nk, o);
+      __builtin_amdgcn_sched_barrier(0);
+      wait_vmcnt<8>();  // this wave's loads of k-tile t + 3
+      lds_barrier();
+    }
+  }
+  if (t < nk) {  // an odd last k-tile
+    const Ops o = ops_of(nk - 1, (t + 4) % kSlots);
+    pin(o);
+    __builtin_amdgcn_sched_barrier(0);
+    step(f0, f1, 0, false, o);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  wait_vmcnt<0>();
+  lds_barrier();
+
+  const int row0 = m0 + grp * 64, col0 = n0 + gw * 32;
+  unsigned* cnt = nullptr;
+  if constexpr (kSplit) {
+    const __amdgpu_buffer_rsrc_t prsrc =
+        __builtin_amdgcn_make_buffer_rsrc(part, 0, (int)((size_t)units * kSlotBytes), kBufferWord3);
+    const SkPlan plan{0, units, pieces, chunks};
+    auto part_off = [&](int qq) {
+      return (uint32_t)((size_t)sk_unit_of(plan, tiles_m * tiles_n, w.tile, qq) * kSlotBytes) +
+             (uint32_t)wave * kWaveSlotBytes;
+    };
+    cnt = counters + (size_t)w.tile * kSkWaves + wave;
+    if (!split_arrive(acc, w.np, w.p, lane, prsrc, part_off, cnt)) return;
+    split_sum(acc, w.np, w.p, lane, prsrc, part_off);
+  }
+
+  const uint32_t wstage = lds_base + wave * Epi<OutT>::kRegion;
+#pragma unroll
+  for (int i = 0; i < 4; i++)
+#pragma unroll
+    for (int j = 0; j < 2; j++) Epi<OutT>::stage(wstage, lane, i, j, acc[i][j]);
+  wait_lgkmcnt0();  // a wave reads back only its own region
+  if constexpr (kEdge)
+    Epi<OutT>::store_edge(wstage, C, M, N, row0, col0, lane);
+  else
+    Epi<OutT>::store(wstage, C + (size_t)row0 * N + col0, N, lane);
+  if constexpr (kSplit) {
+    if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+template <typename OutT, bool kEdge, bool kSplit>
+hipError_t launch_t(const GemmArgs& a, const SkPlan& p) {
+  static std::atomic<uint64_t> attr_done{0};
+  auto kfn = f16_pp128n_kernel<OutT, kEdge, kSplit>;
+  hipError_t e = ensure_lds_attr(kfn, kLdsBytes, a.device, attr_done);
+  if (e != hipSuccess) return e;
+  unsigned* counters = nullptr;
+  float* part = nullptr;
+  if constexpr (kSplit) {
+    counters = static_cast<unsigned*>(a.workspace);
+    part = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + kSkCounterBytes);
+    if (!a.workspace_clean) {
+      e = zero_words(counters, kSkCounterBytes / sizeof(unsigned), a.stream);
+      if (e != hipSuccess) return e;
+    }
+  }
+  hipLaunchKernelGGL(kfn, dim3((unsigned)(kSplit ? p.units : p.dp)), dim3(kThreads), kLdsBytes, a.stream,
+                     static_cast<const half_t*>(a.A), static_cast<const half_t*>(a.B), static_cast<OutT*>(a.C),
+                     (int)a.m, (int)a.n, (int)a.k, p.units, p.pieces, p.chunks, part, counters);
+  return hipGetLastError();
+}
+
+template <typename OutT>
+hipError_t launch_out(const GemmArgs& a) {
+  const SkPlan p = plan_of(a.m, a.n, a.k, a.num_cus);
+  const bool grid = a.m % kBM == 0 && a.n % kBN == 0 && a.k % kBK == 0;
+  if (p.units > 0) return grid ? launch_t<OutT, false, true>(a, p) : launch_t<OutT, true, true>(a, p);
+  return grid ? launch_t<OutT, false, false>(a, p) : launch_t<OutT, true, false>(a, p);
+}
+
+hipError_t launch(const GemmArgs& a) {
+  return a.out_dtype == VK_DTYPE_F16 ? launch_out<half_t>(a) : launch_out<float>(a);
+}
+
+}  // namespace pp128n
 }  // namespace pp128
 }  // namespace
 
@@ -916,6 +1229,15 @@ void register_f16_pp128() {
   e12.caps.uses_workspace = 1;
   e12.launch = pp128::pp128w::launch;
   register_kernel(e12);
+
+  KernelEntry e13 = e12;
+  e13.version = 13;
+  e13.name = "f16_v13_pp128_both";
+  e13.caps = make_caps(13, VK_DTYPE_F16, kOutF16 | kOutF32, 1, 8, 8, 16, pp128::kBM, pp128::kBN,
+                       pp128::pp128n::kBK, pp128::kThreads, pp128::pp128n::kLdsBytes, 0, 0);
+  e13.caps.uses_workspace = 1;
+  e13.launch = pp128::pp128n::launch;
+  register_kernel(e13);
 }
 
 }  // namespace vk
