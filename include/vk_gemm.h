@@ -124,7 +124,7 @@ int vk_gemm_noalloc(int version, vk_dtype in_dtype, vk_dtype out_dtype, size_t m
                     const void* A, const void* B, void* C, void* stream);
 
 /* Workspace bytes a call of this version and shape needs on the current
- * device (0: none).  Versions 8 to 13 depend on the device's
+ * device (0: none).  Versions 8 to 14 depend on the device's
  * compute-unit count;
  * with no device to ask, an MI355X's 256 CUs are assumed.  No counterpart in
  * the reference, whose versions keep such buffers in function-local statics

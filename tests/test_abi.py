@@ -131,9 +131,34 @@ def test_single_hip_runtime_in_process():
     assert len(_abi.hip_runtimes_loaded()) == 1, _abi.hip_runtimes_loaded()
 
 
+def test_workspace_bytes_version14():
+    """Version 14's split plan on 256 CUs: ks = the largest power of two up
+    to 8 with ceil(N / 64) * ks workgroups on the CUs and at least 8 k-steps
+    of 32 per workgroup; the workspace is 4 KB of counters plus ks pieces x
+    the column blocks x 4 waves x 1 KB per 16-row block."""
+    from vibekernel_amd import _abi
+    f16 = _abi.DTYPE_F16
+    ws = lambda m, n, k: _abi.workspace_bytes(14, f16, m, n, k)
+    assert ws(128, 8192, 8192) == 4096 + 2 * 128 * 4 * 8 * 1024   # 128 column blocks x 2
+    assert ws(16, 8192, 8192) == 4096 + 2 * 128 * 4 * 1 * 1024
+    assert ws(64, 4096, 4096) == 4096 + 4 * 64 * 4 * 4 * 1024     # 64 x 4
+    assert ws(100, 2048, 4096) == 4096 + 8 * 32 * 4 * 7 * 1024    # 32 x 8
+    assert ws(64, 264, 1024) == 4096 + 4 * 5 * 4 * 4 * 1024       # 8 steps per piece at ks = 4
+    assert ws(128, 16384, 4096) == 0   # 256 column blocks: one per CU already
+    assert ws(96, 8192, 1056) == 0     # 33 steps: K not split evenly in 2
+    assert ws(17, 72, 160) == 0        # 5 steps: fewer than 8 per piece
+
+
 def test_pick_version_follows_shape():
     import vibekernel_amd as vk
     assert vk.pick_version(16, 8192, 8192) == 8
+    assert vk.pick_version(16, 4096, 4096) == 14   # 2048 < N <= 4096: K split over the waves too
+    assert vk.pick_version(128, 3072, 2048) == 14
+    assert vk.pick_version(128, 2048, 8192) == 14  # N <= 2048 from 65 rows
+    assert vk.pick_version(64, 2048, 8192) == 8
+    assert vk.pick_version(16, 1024, 2048) == 8
+    assert vk.pick_version(1, 5120, 4096) == 8     # 80 column blocks of 64 x 2 pieces: CUs idle
+    assert vk.pick_version(16, 4104, 4096) == 8    # just past N = 4096
     assert vk.pick_version(16, 8224, 8192) == 8  # n % 128 != 0: the last column block cut short
     assert vk.pick_version(16, 8220, 8192) == 1  # n % 8 != 0: the any-shape kernel
     assert vk.pick_version(128, 8192, 8192) == 8  # batch-128 decode: still the split-K kernel

@@ -11,6 +11,9 @@ pytestmark = pytest.mark.gpu
 
 F16_CASES = [
     ((1, 256, 64), 8),           # one row: the skinny split-K kernel
+    ((16, 4096, 4096), 14),      # 2048 < N <= 4096: K split over the waves of a workgroup too
+    ((100, 3000, 2048), 14),     # a last column block of 56 columns
+    ((128, 2048, 8192), 14),     # N <= 2048 from 65 rows
     ((160, 1024, 2048), 8),      # 2 x 2 waves
     ((200, 1024, 2048), 11),     # from 192 rows: 128 x 128 tiles (off the grid, K split)
     ((16, 8224, 256), 8),        # n % 128 != 0: the last column block cut short

@@ -3,8 +3,9 @@ the library's static device scratch array), checked through the C ABI
 against vk_gemm on the same inputs -- bit-identical, since both run the same
 kernels with the same plans -- on two calls in a row, the second with a
 smaller input, for each version that uses a workspace (8: split-K skinny,
-9: split tail, 10: split tail with edges, 11: split of an under-filled grid)
-and one that uses none (7)."""
+9: split tail, 10: split tail with edges, 11: split of an under-filled grid,
+14: K split over the waves of a workgroup and over workgroups) and one that
+uses none (7)."""
 import ctypes
 
 import numpy as np
@@ -19,6 +20,7 @@ CASES = [
     (9, [(2048, 2048, 4096), (512, 512, 8192)]),
     (10, [(1000, 1000, 4000), (257, 520, 4096)]),
     (11, [(512, 4096, 4096), (200, 296, 2000)]),
+    (14, [(128, 4096, 4096), (16, 2048, 8192)]),
     (7, [(1024, 768, 512), (256, 256, 64)]),
 ]
 

@@ -53,6 +53,7 @@ void init_registry() {
     register_f16_pingpong();
     register_f16_pp128();
     register_f16_skinny_sk();
+    register_f16_skinny_wk();
     register_f32_valu();
     register_f32_mfma();
   });

@@ -59,6 +59,7 @@ void register_f16_skinny();
 void register_f16_pingpong();
 void register_f16_pp128();
 void register_f16_skinny_sk();
+void register_f16_skinny_wk();
 void register_f32_valu();
 void register_f32_mfma();
 

@@ -112,7 +112,8 @@ def _num_cus() -> int:
 def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = None) -> int:
     """The fastest version that accepts this shape (checked with vk_gemm_check
     on 4 KiB-aligned placeholder addresses; nothing is launched): for fp16
-    the skinny kernels when M < 192 (version 8; version 4 up to 64), then the
+    the skinny kernels when M < 192 (version 14 where it suits, else version
+    8; version 4 up to 64), then the
     128 x 128 tiles of version 11 where they suit the grid, then the 256x256 kernels
     (fastest first; version 10 takes shapes off the 256 x 256 x 64 grid
     whose N and K are multiples of 8), then the any-shape kernel.  Version 11
@@ -136,6 +137,19 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
     the two trade places with N and K (M = 128: 128 x 4096 x 4096 18.5
     against 21.7, 128 x 4096 x 14336 39.1 against 34.4), and version 8 keeps
     them.
+    Version 14 (K split over the waves of a workgroup, 64-column blocks) is
+    taken up to M = 64 where 2048 < N <= 4096, and from M = 65 to 128 where
+    N <= 4096 and K <= 4096, or N <= 2048 and K <= 8192.  Measured on MI355X
+    against version 8 (us per launch, one box, M = 1 / 16 / 64 / 128):
+    N = 4096, K = 4096 8.1 / 9.1 / 14.4 / 18.4 against 9.5 / 9.9 / 16.2 /
+    21.8; N = 3072, K = 2048 7.2 / 7.6 / 11.6 / 14.4 against 8.1 / 8.3 /
+    13.5 / 20.3; N = 4096, K = 14336 22.1 / 22.9 / 27.1 / 39.0 against
+    22.2 / 22.5 / 28.5 / 35.3; N = 2048, K = 8192 at M = 128 21.0 against
+    23.4, at M = 16 10.2 against 10.5; N = 1024, K = 2048 8.3 / 8.6 / 12.4 /
+    15.9 against 6.7 / 7.0 / 10.9 / 17.6.  Every 64 columns re-read all of
+    A (at M = 128 twice B's bytes), which costs it at large M and K; from
+    N = 5120 its power-of-two K split also leaves CUs idle (80 column blocks
+    x 2): 128 x 8192 x 8192 41.8 against 32.9.
     The split-tail version 9 comes first among the 256x256 kernels only where
     its schedule splits tiles on this device (it then needs a workspace);
     elsewhere it would run version 7's whole tiles.  The reference picks
@@ -143,7 +157,7 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
     convenience of the front end."""
     in_dt = DTYPE_F16 if dtype == "f16" else DTYPE_F32
     out_dt = DTYPE_F16 if (out or dtype) == "f16" else DTYPE_F32
-    order = [8, 4, 11, 9, 7, 10, 6, 5, 3, 2, 1] if in_dt == DTYPE_F16 else [2, 3, 1]
+    order = [14, 8, 4, 11, 9, 7, 10, 6, 5, 3, 2, 1] if in_dt == DTYPE_F16 else [2, 3, 1]
     avail = set(_abi.versions(in_dt))
 
     def takes(v):
@@ -156,8 +170,17 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
             return tiles <= cus
         return 2 * tiles <= 3 * cus
 
+    def v14_suits():
+        if m > 128 or n > 4096:
+            return False
+        if m <= 64:
+            return n > 2048
+        return k <= 4096 or (n <= 2048 and k <= 8192)
+
     for v in order:
         if v not in avail:
+            continue
+        if v == 14 and not v14_suits():
             continue
         if v == 8 and m >= 192 and in_dt == DTYPE_F16 and v11_suits() and takes(11):
             continue
