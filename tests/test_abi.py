@@ -133,8 +133,9 @@ def test_single_hip_runtime_in_process():
 
 def test_workspace_bytes_version14():
     """Version 14's split plan on 256 CUs: ks = the largest power of two up
-    to 8 with ceil(N / 64) * ks workgroups on the CUs and at least 8 k-steps
-    of 32 per workgroup; the workspace is 4 KB of counters plus ks pieces x
+    to 8 that keeps ceil(N / 64) * ks workgroups on the CUs with at least 8
+    k-steps of 32 per piece, or more pieces where they fill idle CUs with at
+    least 32 steps each; the workspace is 4 KB of counters plus ks pieces x
     the column blocks x 4 waves x 1 KB per 16-row block."""
     from vibekernel_amd import _abi
     f16 = _abi.DTYPE_F16
@@ -145,7 +146,10 @@ def test_workspace_bytes_version14():
     assert ws(100, 2048, 4096) == 4096 + 8 * 32 * 4 * 7 * 1024    # 32 x 8
     assert ws(64, 264, 1024) == 4096 + 4 * 5 * 4 * 4 * 1024       # 8 steps per piece at ks = 4
     assert ws(128, 16384, 4096) == 0   # 256 column blocks: one per CU already
-    assert ws(96, 8192, 1056) == 0     # 33 steps: K not split evenly in 2
+    assert ws(96, 8192, 1056) == 4096 + 2 * 128 * 4 * 6 * 1024    # 33 steps: pieces of 16 and 17
+    assert ws(1, 5120, 4096) == 4096 + 3 * 80 * 4 * 1 * 1024      # 80 x 3 = 240 workgroups, 42 steps each
+    assert ws(16, 3072, 4096) == 4096 + 4 * 48 * 4 * 1 * 1024     # 5 pieces would have 25 steps
+    assert ws(48, 1000, 2016) == 4096 + 4 * 16 * 4 * 3 * 1024     # 63 steps: at least 8 per piece
     assert ws(17, 72, 160) == 0        # 5 steps: fewer than 8 per piece
 
 

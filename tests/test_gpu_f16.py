@@ -23,7 +23,8 @@ SKINNY_SHAPES = [(16, 256, 512), (32, 512, 1024), (48, 96, 128), (64, 128, 256),
                  (80, 256, 512), (96, 384, 96), (112, 128, 1024), (128, 1024, 2048),
                  (1, 128, 32), (5, 256, 512), (17, 384, 1024), (144, 256, 512), (170, 512, 1024),
                  (176, 128, 96), (161, 1024, 2048), (200, 512, 1024), (250, 128, 96), (256, 1024, 2048),
-                 (1, 4000, 512), (16, 1000, 256), (200, 264, 1024), (33, 8, 64)]
+                 (1, 4000, 512), (16, 1000, 256), (200, 264, 1024), (33, 8, 64),
+                 (16, 2048, 4064), (100, 1024, 2016)]  # K split in unequal pieces
 
 
 def _versions():

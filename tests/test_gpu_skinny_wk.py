@@ -6,7 +6,8 @@ through per-(column block, wave) counters).
 Shapes cover 1 to 8 row blocks (the register rings change at 5), k-step
 counts that leave waves with no step, with whole rings of steps and with
 steps of zeros padding the last ring, column blocks that N cuts short, and
-ks = 1, 2, 4 and 8 (the CPU test of the plan is tests/test_abi.py).  Bars: small-integer
+ks = 1, 2, 4 and 8, with pieces of equal and unequal step counts (the CPU test of the plan
+is tests/test_abi.py).  Bars: small-integer
 inputs bit-exact (every partial sum is an integer below 2^24, so any step
 dropped, doubled, or taken by two waves or two pieces changes the result);
 N(0,1) inputs within the fp32 accumulation bound (fp16 output: plus half an
@@ -30,18 +31,19 @@ SHAPES = [
     (17, 72, 160),      # N cut (8 of 64 columns in the second block)
     (33, 200, 416),     # 13 k-steps: remainders of the 6-step ring
     (64, 264, 1024),    # ks = 4, 2 steps per wave; 4 row blocks (ring of 6)
-    (65, 136, 1088),    # 5 row blocks (ring of 4)
+    (65, 136, 1088),    # 5 row blocks (ring of 4); 34 steps in 4 pieces of 8 or 9
     (100, 136, 2048),   # 7 row blocks
     (128, 128, 4096),   # ks = 8
-    (96, 8192, 1056),   # 33 k-steps, unsplit: 9 / 8 steps per wave
-    (48, 1000, 2016),   # last column block of 40 columns; 63 k-steps
+    (96, 8192, 1056),   # 33 k-steps in pieces of 16 and 17
+    (48, 1000, 2016),   # last column block of 40 columns; 63 k-steps in 4 pieces of 15 or 16
     (5, 8, 8192),       # one 8-column block, ks = 8
-    (128, 520, 4064),   # 127 k-steps
+    (128, 520, 4064),   # 127 k-steps in 8 pieces of 15 or 16
+    (64, 5120, 4096),   # 80 column blocks x 3 pieces of 42 or 43 steps
     (112, 2048, 4096),  # ks = 8 over 32 column blocks
     (128, 8192, 8192),  # batch-128 decode: ks = 2
 ]
 SPLIT = {(64, 264, 1024), (128, 128, 4096), (5, 8, 8192), (112, 2048, 4096), (128, 8192, 8192), (100, 136, 2048),
-         (65, 136, 1088)}
+         (65, 136, 1088), (96, 8192, 1056), (48, 1000, 2016), (128, 520, 4064), (64, 5120, 4096)}
 
 
 def _ws(v, m, n, k):

@@ -10,9 +10,10 @@
 // strip 6.4 TB/s, 256-byte strips with K split over 4 workgroups 6.7 TB/s.
 // Version 4 owns 64-byte strips.  Here:
 //  * a workgroup owns NC = 128 columns (256-byte rows of B; the kernel is
-//    written for NC = 256 as well) and 1/KS of K; grid = ceil(N / NC) x KS with
-//    KS the largest power of two (up to 8) that keeps the grid within one
-//    workgroup per CU (KS = 4 at N = 8192 on 256 CUs);
+//    written for NC = 256 as well) and 1/KS of K (pieces of whole 32-deep
+//    steps); grid = ceil(N / NC) x KS with KS the largest power of two (up
+//    to 8) that keeps the grid within one workgroup per CU (KS = 4 at
+//    N = 8192 on 256 CUs);
 //  * 4 waves; per 32-deep k-step each wave loads 8 rows of B (direct-to-LDS,
 //    1 KB per instruction) and wave w the 16-row blocks w and w + 4 of A that
 //    exist (MB = M / 16 blocks); a ring of up to 8 stages (6-7 k-steps of B
@@ -44,6 +45,7 @@
 #include "vk_internal.hpp"
 #include "vk_tile.hpp"
 
+#include <algorithm>
 #include <atomic>
 #include <type_traits>
 
@@ -102,19 +104,25 @@ int pick_nc(size_t) { return 128; }
 // Counters of the split-K hand-off, one per (column block, wave).
 constexpr size_t kCounterBytes = 4096;
 
-// Number of workgroups sharing a column block's K range: the largest power
-// of two up to 8 that keeps the grid to one workgroup per CU and divides K
-// into 32-deep steps.  Measured (us per launch, K split 1/2/4/8 ways):
-// 128 x 28672 x 8192 (224 column blocks): 118 / 133 / 154 / 192;
-// 128 x 11008 x 4096 (86): 46 / 29 / 37 / 52; 32 x 14336 x 4096 (112):
-// 23 / 21 / 25 / 36; 128 x 8192 x 8192 (64): 86 / 49 / 33 / 54 -- a second
-// round of workgroups costs more than the longer k range of each.
+// Number of workgroups sharing a column block's K range (pieces of K / 32
+// steps, as equal as the steps allow): the largest power of two up to 8 that
+// keeps the grid to one workgroup per CU with at least 4 steps per piece,
+// while the counters fit.  Measured (us per launch, K split 1/2/4/8 ways):
+// 128 x 28672 x 8192 (224 column blocks): 118 / 133 / 154 / 192; 128 x
+// 11008 x 4096 (86): 46 / 29 / 37 / 52; 32 x 14336 x 4096 (112): 23 / 21 /
+// 25 / 36; 128 x 8192 x 8192 (64): 86 / 49 / 33 / 54 -- a second round of
+// workgroups costs more than the longer k range of each.  Counts between
+// the powers of two fill more CUs and lose (5120 x 4096 at M = 1 / 16 / 64 /
+// 128 with 6 pieces instead of 4: 13.3 / 13.5 / 16.6 / 21.8 against 11.2 /
+// 11.2 / 14.4 / 20.3; 4608 x 4096 with 7: 12.2 / 12.8 / 18.2 / 22.4 against
+// 10.3 / 10.5 / 13.6 / 19.9): their partials and longer sums cost more.
+// Unequal pieces split K that 32 ks does not divide (128 x 8192 x 4064 in
+// 4: 23.4 against 36.0 unsplit).
 int pick_ks(size_t n, size_t k, int num_cus) {
   const size_t ncb = (n + pick_nc(n) - 1) / pick_nc(n);
+  if (ncb * kWaves * sizeof(unsigned) > kCounterBytes) return 1;
   int ks = 1;
-  while (ks < 8 && ncb * ks * 2 <= (size_t)num_cus && k % ((size_t)kKStep * ks * 2) == 0 &&
-         ncb * kWaves * sizeof(unsigned) <= kCounterBytes)
-    ks *= 2;
+  while (ks < 8 && ncb * ks * 2 <= (size_t)num_cus && k / kKStep / (ks * 2) >= 4) ks *= 2;
   return ks;
 }
 
@@ -133,9 +141,11 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
   const int cid = blockIdx.x;
   const int cb = cid / ks_count, kp = cid - cb * ks_count;
   const int n0 = cb * NC;
-  const int kc = K / ks_count;  // k rows of this workgroup
-  const int kbeg = kp * kc;
-  const int nsteps = kc / kKStep;
+  // Piece kp of the K / 32 steps: steps floor(kp T / ks) .. floor((kp + 1) T / ks) - 1.
+  const int tsteps = K / kKStep;
+  const int sbeg = (int)((long long)kp * tsteps / ks_count);
+  const int kbeg = sbeg * kKStep;
+  const int nsteps = (int)((long long)(kp + 1) * tsteps / ks_count) - sbeg;
 
   // Direct-to-LDS duty per k-step.  B: load i covers k-rows 8w + i*R .. +R-1
   // (R = 1024 / (2 NC) rows of NC/8 chunks; lane l: row l / (NC/8), slot
@@ -353,7 +363,11 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
   };
   switch (ks_count) {
     case 2: fold(std::integral_constant<int, 2>{}); break;
+    case 3: fold(std::integral_constant<int, 3>{}); break;
     case 4: fold(std::integral_constant<int, 4>{}); break;
+    case 5: fold(std::integral_constant<int, 5>{}); break;
+    case 6: fold(std::integral_constant<int, 6>{}); break;
+    case 7: fold(std::integral_constant<int, 7>{}); break;
     default: fold(std::integral_constant<int, 8>{}); break;
   }
   if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

@@ -9,10 +9,12 @@
 // its k-loop (per-workgroup timelines: 23.9 us of k-loop where the B stream
 // alone takes ~20), and 4 k pieces per column block hand 12 MB of fp32
 // partials from workgroup to workgroup at N = K = 8192.  Here:
-//  * a workgroup owns NC = 64 columns (128-byte rows of B) and 1/ks of K;
-//    grid = ceil(N / 64) x ks, ks the largest power of two (up to 8) that
-//    keeps one workgroup per CU (ks = 2 at N = 8192 on 256 CUs: the partials
-//    are 4 MB);
+//  * a workgroup owns NC = 64 columns (128-byte rows of B) and 1/ks of K
+//    (pieces of whole 32-deep steps); grid = ceil(N / 64) x ks, ks a power
+//    of two up to 8 that keeps one workgroup per CU, or more where that
+//    fills idle CUs with pieces of at least 32 steps (ks = 2 at N = 8192 on
+//    256 CUs: the partials are 4 MB; 3 at N = 5120, K = 4096: 80 column
+//    blocks x 3 on 240 CUs);
 //  * wave w computes the workgroup's whole M x 64 block over k-steps (32
 //    deep) w, w + 4, w + 8, ... of the workgroup's range, on its own: its
 //    own loads, its own LDS ring, no barrier in the k-loop.  Every byte of A
@@ -43,6 +45,7 @@
 #include "vk_internal.hpp"
 #include "vk_tile.hpp"
 
+#include <algorithm>
 #include <atomic>
 #include <type_traits>
 
@@ -55,6 +58,7 @@ constexpr int kKStep = 32;                 // k per step (one 16x16x32 MFMA deep
 constexpr int kMaxRows = 128;
 constexpr int kNC = 64;                    // columns per workgroup
 constexpr size_t kCounterBytes = 4096;     // (column block, wave) counters
+constexpr int kMaxPieces = 8;              // K pieces per column block
 
 // MB 16-row blocks.
 template <int MB>
@@ -120,9 +124,11 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_wk_kernel(const half_t
 
   const int cb = blockIdx.x / ks_count, kp = blockIdx.x - cb * ks_count;
   const int n0 = cb * kNC;
-  const int kc = K / ks_count;      // k rows of this workgroup
-  const int kbeg = kp * kc;
-  const int nsteps = kc / kKStep;   // k-steps of this workgroup
+  // Piece kp of the K / 32 steps: steps floor(kp T / ks) .. floor((kp + 1) T / ks) - 1.
+  const int tsteps = K / kKStep;
+  const int sbeg = (int)((long long)kp * tsteps / ks_count);
+  const int kbeg = sbeg * kKStep;
+  const int nsteps = (int)((long long)(kp + 1) * tsteps / ks_count) - sbeg;  // k-steps of this workgroup
   const int ns = nsteps > wave ? (nsteps - wave + kWaves - 1) / kWaves : 0;  // this wave's steps
   const int ns_pad = (ns + S - 1) / S * S;  // plus steps of zeros
   const uint32_t lbase = lds_addr32(lds);
@@ -327,9 +333,14 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_wk_kernel(const half_t
       }
     }
   };
+  static_assert(kMaxPieces == 8, "one case per piece count");
   switch (ks_count) {
     case 2: fold(std::integral_constant<int, 2>{}); break;
+    case 3: fold(std::integral_constant<int, 3>{}); break;
     case 4: fold(std::integral_constant<int, 4>{}); break;
+    case 5: fold(std::integral_constant<int, 5>{}); break;
+    case 6: fold(std::integral_constant<int, 6>{}); break;
+    case 7: fold(std::integral_constant<int, 7>{}); break;
     default: fold(std::integral_constant<int, 8>{}); break;
   }
   if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -337,16 +348,24 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_wk_kernel(const half_t
 
 int wk_mb(size_t m) { return (int)((m + 15) / 16); }
 
-// Workgroups sharing a column block's K range: the largest power of two up
-// to 8 that keeps the grid to one workgroup per CU, divides K into 32-deep
-// steps with at least 8 per workgroup (2 per wave), and keeps the counters
-// in their 4 KB.
+// Workgroups sharing a column block's K range (pieces of K / 32 steps, as
+// equal as the steps allow), while the counters fit their 4 KB: the largest
+// power of two up to 8 that keeps the grid to one workgroup per CU with at
+// least 8 steps per piece (2 per wave); or, where that leaves CUs idle, as
+// many as fill them if the pieces keep at least 32 steps.  Measured (us per
+// launch, one box, M = 1 / 16 / 64 / 128): 5120 x 4096 in 3 pieces 12.5 /
+// 12.5 / 16.8 / 21.6 against 12.7 / 13.2 / 19.4 / 26.7 in 2; 5120 x 8192
+// 18.3 / 19.0 / 24.4 / 34.1 against 19.4 / 21.3 / 31.1 / 45.3; but 2560 x
+// 4096 in 6 pieces of 21 steps 8.0 / 8.7 / 13.6 / 18.1 against 7.1 / 8.0 /
+// 12.6 / 17.9 in 4: short pieces cost more in partials than the CUs gain.
 int wk_pick_ks(size_t n, size_t k, int num_cus) {
   const size_t ncb = (n + kNC - 1) / kNC;
+  if (ncb * kWaves * sizeof(unsigned) > kCounterBytes) return 1;
+  const size_t steps = k / kKStep;
   int ks = 1;
-  while (ks < 8 && ncb * ks * 2 <= (size_t)num_cus && k % ((size_t)kKStep * ks * 2) == 0 &&
-         k / ((size_t)kKStep * ks * 2) >= 8 && ncb * kWaves * sizeof(unsigned) <= kCounterBytes)
-    ks *= 2;
+  while (ks < kMaxPieces && ncb * ks * 2 <= (size_t)num_cus && steps / (ks * 2) >= 8) ks *= 2;
+  const size_t fill = std::min<size_t>(kMaxPieces, (size_t)num_cus / ncb);
+  if (fill > (size_t)ks && steps / fill >= 32) ks = (int)fill;
   return ks;
 }
 
