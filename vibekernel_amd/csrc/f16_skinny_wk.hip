@@ -360,7 +360,7 @@ int wk_mb(size_t m) { return (int)((m + 15) / 16); }
 // 12.6 / 17.9 in 4: short pieces cost more in partials than the CUs gain.
 int wk_pick_ks(size_t n, size_t k, int num_cus) {
   const size_t ncb = (n + kNC - 1) / kNC;
-  if (ncb * kWaves * sizeof(unsigned) > kCounterBytes) return 1;
+  if (ncb == 0 || ncb * kWaves * sizeof(unsigned) > kCounterBytes) return 1;
   const size_t steps = k / kKStep;
   int ks = 1;
   while (ks < kMaxPieces && ncb * ks * 2 <= (size_t)num_cus && steps / (ks * 2) >= 8) ks *= 2;
