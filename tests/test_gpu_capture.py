@@ -1,8 +1,10 @@
-"""Stream capture (HIP graphs) of the C ABI: a split call on 1000 x 1000 x
-4000 (version 10, whose tail tiles are cut into pieces that meet through a
+"""Stream capture (HIP graphs) of the C ABI: a split call (1000 x 1000 x 4000
+on version 10, whose tail tiles are cut into pieces that meet through a
 workspace, and version 11, whose 64 tiles of 128 x 128 are each cut into 4
-k-slices) captured with a caller workspace (vk_gemm_ws) and replayed several
-times, with eager work and synchronisations between the replays, each replay
+k-slices; 64 x 2048 x 4096 on the skinny version 8, K in 8 pieces; 128 x
+4096 x 4096 on version 14, K in 4 pieces over workgroups and 4 over each
+workgroup's waves) captured with a caller workspace (vk_gemm_ws) and
+replayed several times, with eager work and synchronisations between the replays, each replay
 bit-identical to the eager call and within the fp32 bound of the exact
 product; the same call through the library workspace (vk_gemm) is refused
 under capture; a version with no workspace captures through vk_gemm."""
@@ -19,19 +21,20 @@ def _ptr(t):
     return ctypes.c_void_p(t.data_ptr())
 
 
-@pytest.mark.parametrize("version", [10, 11])
-def test_split_tail_capture_and_replay(gpu, oracle, version):
+@pytest.mark.parametrize("version,shape", [(10, (1000, 1000, 4000)), (11, (1000, 1000, 4000)),
+                                           (8, (64, 2048, 4096)), (14, (128, 4096, 4096))])
+def test_split_tail_capture_and_replay(gpu, oracle, version, shape):
     import torch
     import vibekernel_amd as vk
     from vibekernel_amd import _abi
-    m, n, k = 1000, 1000, 4000
+    m, n, k = shape
     A, B = make_inputs(m, n, k, "uniform", seed=31)
     tA, tB = torch.from_numpy(A).cuda(), torch.from_numpy(B).cuda()
     need = _abi.workspace_bytes(version, vk.DTYPE_F16, m, n, k)
     assert need > 0  # the plan splits this shape
     ws = torch.empty(need, dtype=torch.uint8, device="cuda:0")
     C_eager = torch.full((m, n), float("nan"), dtype=torch.float16, device="cuda:0")
-    announce(f"capture: eager v{version} 1000x1000x4000 with caller workspace")
+    announce(f"capture: eager v{version} {m}x{n}x{k} with caller workspace")
     s = torch.cuda.current_stream()
     st = _abi.gemm_ws(version, vk.DTYPE_F16, vk.DTYPE_F16, m, n, k, _ptr(tA), _ptr(tB), _ptr(C_eager),
                       _ptr(ws), need, _ptr_stream(s))
