@@ -23,16 +23,15 @@
 //    (16 rows x 64 bytes per load), and only B, which the MFMA needs
 //    transposed, goes through LDS (direct-to-LDS, 4 KB per k-step, read with
 //    the transpose read);
-//  * loads run D k-steps ahead in the wave (D = 7 up to 64 rows of 64
-//    columns, 3 otherwise, over rings of D + 1 A fragment buffers in
-//    registers and B stages in LDS), all on the in-order vmcnt, waited for
-//    with constant counts; a wave's step count is padded to a multiple of
-//    D + 1 with steps whose
+//  * loads run D k-steps ahead in the wave (D = 7 up to 64 rows, 3 above,
+//    over rings of D + 1 A fragment buffers in registers and B stages in
+//    LDS), all on the in-order vmcnt, waited for with constant counts;
+//  * a wave's step count is padded to a multiple of D + 1 with steps whose
 //    loads lie past the ends of buffer resources sized to A and B (zeros,
 //    no memory touched), so the loop has no remainder (a remainder's second
 //    copy of the body cost the 128-row instance ~330 register moves per
-//    ring), and their products add +0.0 to accumulators that started at
-//    +0.0, which leaves them unchanged;
+//    ring); their products add +0.0 to accumulators that started at +0.0,
+//    which leaves them unchanged;
 //  * after the k-loop the 4 waves' M x 64 fp32 sums meet in LDS, and wave q
 //    adds column block q of the 4 in wave order;
 //  * with K split over workgroups, wave q of each piece hands its M x 16
@@ -136,9 +135,10 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_wk_kernel(const half_t
 
   // B: load i of a step covers k-rows 8i + l / 8 (8 rows of 8 chunks); lane
   // l lands at chunk slot l % 8 and fetches chunk (l % 8) ^ swz(row),
-  // through a buffer resource over the K x N matrix.  In a last column block that N cuts short (N a multiple of 8) a
-  // chunk past N is replaced by the block's last valid chunk of the same
-  // row: valid memory, and the columns past N are never stored.
+  // through a buffer resource over the K x N matrix.  In a last column block
+  // that N cuts short (N a multiple of 8) a chunk past N is replaced by the
+  // block's last valid chunk of the same row: valid memory, and the columns
+  // past N are never stored.
   const int cvalid = min(kNC, N - n0) / 8;
   uint32_t offB[G::kBLoads];
 #pragma unroll
