@@ -1,8 +1,8 @@
 """ctypes front end of the CPU oracle (oracle/vk_oracle.c).
 
-TEST INFRASTRUCTURE ONLY: imported by tests/, by ``__graft_entry__.smoke()``
-to verify its result, and by bench.py's cpu_baseline leg as the timed CPU
-baseline.
+TEST INFRASTRUCTURE ONLY: imported by tests/ and by
+``__graft_entry__.smoke()`` to verify its result.  bench.py's cpu_baseline leg
+times the harness's own version 0 (libvk_v0.so), not this oracle.
 The product never imports it.
 
 Every function follows a reference file (paths relative to the reference

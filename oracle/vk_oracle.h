@@ -3,8 +3,8 @@
  *
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product (the HIP library, the
  * task1 harness, the Python package) may include, link or call this code.
- * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg use it,
- * and only as the checker / the timed CPU baseline.
+ * Only tests/ and __graft_entry__.smoke() use it, and only as the checker
+ * (bench.py's cpu_baseline times the harness's version 0, libvk_v0.so).
  *
  * What it restates (paths relative to the reference repository root):
  *   - v0 fp32:  results/ralph_loop_fable/src/matmul_f32/matmul_f32_v0_cblas.cpp:8-12

@@ -189,3 +189,42 @@ def test_pick_version_follows_shape():
     assert vk.pick_version(512, 512, 512, "f32") == 2   # fp32 on the matrix cores
     assert vk.pick_version(500, 512, 512, "f32") == 3   # m % 256 != 0: the matrix cores with edges
     assert vk.pick_version(500, 510, 512, "f32") == 1   # n % 4 != 0: the VALU kernel
+
+
+def test_pick_version_raises_when_no_version_accepts():
+    """No version takes fp32 input with fp16 output, and none takes a shape
+    whose 32-bit offsets overflow: the pick raises VkError (status -3), not a
+    None that the C-ABI call would reject with a ctypes error."""
+    import vibekernel_amd as vk
+    with pytest.raises(vk.VkError) as e:
+        vk.pick_version(256, 256, 256, "f32", "f16")
+    assert e.value.status == -3
+    with pytest.raises(vk.VkError):
+        vk.pick_version(1 << 24, 3, 8)
+
+
+def test_leave_one_out_instances_registered():
+    """fp16 71-77 are version 7 with one ingredient off: listed by the
+    library, named after version 7, accepting exactly version 7's shapes, and
+    left out of vibekernel_amd.versions() and the pick unless asked for."""
+    import vibekernel_amd as vk
+    from vibekernel_amd import _abi
+    text = open(os.path.join(ROOT, "include", "vk_gemm.h")).read()
+    first = int(re.search(r"#define VK_F16_LEAVE_ONE_OUT_FIRST (\d+)", text).group(1))
+    last = int(re.search(r"#define VK_F16_LEAVE_ONE_OUT_LAST (\d+)", text).group(1))
+    assert list(_abi.LEAVE_ONE_OUT) == list(range(first, last + 1))
+    lib = _abi.versions(_abi.DTYPE_F16)
+    c7 = vk.query(7)
+    for v in _abi.LEAVE_ONE_OUT:
+        assert v in lib
+        assert _abi.name(v, _abi.DTYPE_F16).startswith(f"f16_v{v}_v7_")
+        c = vk.query(v)
+        for f in ("div_m", "div_n", "div_k", "max_m", "align_bytes", "tile", "threads", "out_dtypes",
+                  "uses_workspace", "tolerance_tier"):
+            assert getattr(c, f) == getattr(c7, f), (v, f)
+        assert c.lds_bytes <= 160 * 1024
+        for shape in ((4096, 4096, 4096), (256, 256, 64), (4096, 4096, 4000), (4000, 4096, 4096)):
+            assert _abi.check(v, F16, F16, *shape, P, P, P) == _abi.check(7, F16, F16, *shape, P, P, P)
+        assert v not in vk.versions("f16")
+        assert v in vk.versions("f16", leave_one_out=True)
+    assert vk.pick_version(4096, 4096, 4096) == 7

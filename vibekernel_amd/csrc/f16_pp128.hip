@@ -147,7 +147,8 @@ struct Epi<float> {
 
 // ---- split K for grids whose tiles fill at most half of the CUs ----
 // With T tiles of I k-tiles on C CUs and 2T <= C, each tile is cut into
-// s = min(8, C / T, I / 4) aligned k-slices (at least 4 k-tiles each)
+// s = min(8, C / T, I / 8) aligned k-slices (at least kFillMinIters = 8
+// k-tiles each)
 // computed by s workgroups at once (sk_plan_fill in vk_splittail.hpp: no
 // whole tiles; the pieces of an XCD's share of the raster stay on it), and
 // the pieces of a tile meet as in version 9: per (tile, wave) an arrival

@@ -85,8 +85,13 @@ def gemm(A, B, version: int | None = None, out_dtype=None, stream=None):
     return C
 
 
-def versions(dtype: str = "f16") -> list:
-    return _abi.versions(DTYPE_F16 if dtype == "f16" else DTYPE_F32)
+def versions(dtype: str = "f16", leave_one_out: bool = False) -> list:
+    """The library's versions for an input dtype; the leave-one-out instances
+    of version 7 (fp16 71-77, measurement only) only when asked for."""
+    vs = _abi.versions(DTYPE_F16 if dtype == "f16" else DTYPE_F32)
+    if dtype == "f16" and not leave_one_out:
+        vs = [v for v in vs if v not in _abi.LEAVE_ONE_OUT]
+    return vs
 
 
 def name(version: int, dtype: str = "f16"):
@@ -190,3 +195,4 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
             continue
         if takes(v):
             return v
+    raise VkError(-3, f"no {dtype} version accepts m={m}, n={n}, k={k} with {out or dtype} output")
