@@ -21,18 +21,32 @@ ms_per_step = event time / steps (the mean launch duration);
 value = 2*m*n*k / ms_per_step.  The reference's
 own loop (an event pair and a host sync around every launch, main.cpp:52-62)
 runs afterwards (100 launches; `--no-reference-loop` skips it) and is reported
-as `reference_loop`.  The two differ on MI355X: back to back, the GEMM holds
-the board at its power limit and the clock drops; the idle gaps of the
-synchronised loop let it recover, so its per-launch times are shorter.
+as `reference_loop`.  Its per-launch times are longer on MI355X (measured:
+104.9 us against 93.3 back to back at 4096^3): each holds the host round trip
+of its event synchronisation, which the back-to-back region hides.
 
 Clock: the SCLK, memory clock, socket power and GFX activity are sampled
 from the driver's metrics table on a host thread (libvk_bench.so,
-vkb_clock_*) over the settle phase after its first 300 ms (the same call back
-to back, as in the timed region; the table refreshes about once per second, so
-the 10 ms timed region itself rarely holds a sample), and reported under
-`clock`; `roofline.frac_clock` is the achieved rate over the peak at that
-clock (CUs x FLOP per clock per CU x SCLK), beside `frac` against the spec
-peak at 2.4 GHz.
+vkb_clock_*) from 300 ms into the settle phase until the timed region ends.
+The table refreshes about once per second, so the settle phase ends on a
+refresh: after --settle-ms the same launches continue in ~4 ms chunks until
+the sampler sees a new table, and the timed region starts at once.  Every
+sample is reported under `clock.samples` with its age (host time of the read
+that saw it minus the timed region's start); `roofline.frac_clock` is the
+achieved rate over the peak at the SCLK of the sample nearest the timed
+region's start (CUs x FLOP per clock per CU x SCLK), beside `frac` against
+the spec peak at 2.4 GHz.
+
+Library ceiling (after the timed region, the output check and the reference
+loop; `--no-library-ceiling` skips it; never part of any product path): the
+same product on the same A and B through torch.matmul (fp16 out, fp32
+accumulation) under the same protocol -- a settle phase of the same length
+ending on a metrics refresh, `--warmup` launches, a device synchronisation,
+`--steps` launches back to back between one event pair -- once per BLAS
+backend torch offers on ROCm (hipBLASLt, rocBLAS, Composable Kernel), reported as
+`library_ceiling` with each backend's ms_per_step, SCLK and frac_clock, and
+its output checked against the same bound.  It says how far the chip lets a
+vendor library go at this shape under the same clock conditions.
 
 Other configurations of the same GEMM: `--workload` (see WORKLOADS) or
 explicit --m/--n/--k/--dtype/--dist.
@@ -109,6 +123,11 @@ def parse():
     p.add_argument("--no-reference-loop", action="store_true",
                    help="skip the reference's per-launch synchronised loop after the timed region "
                         "(100 more launches of the same kernel)")
+    p.add_argument("--no-library-ceiling", action="store_true",
+                   help="skip timing torch.matmul (hipBLASLt, rocBLAS, CK) under the same protocol afterwards")
+    p.add_argument("--library-tune", action="store_true",
+                   help="let torch's TunableOp pick the fastest library solution for the shape before "
+                        "the library ceiling is timed (tuning takes some seconds)")
     a = p.parse_args()
     m, n, k, dt, dist = WORKLOADS[a.workload]
     a.m = a.m or m
@@ -161,7 +180,16 @@ def load_bench_lib():
     L.vkb_clock_stop.argtypes = [ctypes.POINTER(ClockStats)]
     L.vkb_clock_stop.restype = ci
     L.vkb_clock_error.restype = ctypes.c_char_p
+    L.vkb_clock_samples.argtypes = [ctypes.POINTER(ClockSample), ci]
+    L.vkb_clock_samples.restype = ci
+    L.vkb_clock_now_ms.restype = ctypes.c_double
     return L
+
+
+class ClockSample(ctypes.Structure):
+    """vkb_clock_sample (include/vk_bench.h)."""
+    _fields_ = [("t_ms", ctypes.c_double), ("gfx_mhz", ctypes.c_double), ("uclk_mhz", ctypes.c_double),
+                ("socket_w", ctypes.c_double), ("gfx_activity", ctypes.c_double)]
 
 
 class ClockStats(ctypes.Structure):
@@ -191,6 +219,178 @@ class Clock:
                 "sclk_mhz_max": round(st.gfx_mhz_max, 1), "mclk_mhz": round(st.uclk_mhz_mean, 1),
                 "socket_w": round(st.socket_w_mean, 1), "gfx_busy_pct": round(st.gfx_activity_mean, 1),
                 "samples": st.samples, "window_ms": round(st.window_ms, 2)}
+
+    def count(self):
+        return self.lib.vkb_clock_samples(None, 0) if self.ok else 0
+
+    def now_ms(self):
+        return self.lib.vkb_clock_now_ms()
+
+    def samples(self):
+        n = self.count()
+        if n <= 0:
+            return []
+        buf = (ClockSample * n)()
+        n = min(n, self.lib.vkb_clock_samples(buf, n))
+        return [buf[i] for i in range(n)]
+
+
+def _aggregate(samples):
+    """Mean SCLK, memory clock, socket power and GFX activity of samples."""
+    if not samples:
+        return None
+    g = [s.gfx_mhz for s in samples]
+    u = [s.uclk_mhz for s in samples if s.uclk_mhz > 0]
+    w = [s.socket_w for s in samples if s.socket_w > 0]
+    b = [s.gfx_activity for s in samples if s.gfx_activity >= 0]
+    mean = lambda xs: round(sum(xs) / len(xs), 1) if xs else None  # noqa: E731
+    return {"sclk_mhz": mean(g), "sclk_mhz_min": round(min(g), 1), "sclk_mhz_max": round(max(g), 1),
+            "mclk_mhz": mean(u), "socket_w": mean(w), "gfx_busy_pct": mean(b), "samples": len(samples)}
+
+
+def measure(clock, chunk, timed, settle_ms, per_launch_ms_hint=0.1):
+    """The timed protocol for one launch sequence.
+
+    chunk(n) runs n launches back to back and returns their event time in ms
+    (synchronised); timed() runs the timed region (warm-up, device sync,
+    steps back to back between one event pair) and returns its event time in
+    ms.  Settle phase: chunks of ~50 ms until settle_ms have passed on the
+    host clock, the sampler running from min(300 ms, settle_ms / 2) on; then
+    chunks of ~4 ms until the sampler sees a metrics refresh (at most 1.5 s
+    more), and the timed region starts at once.  Returns (timed ms, record)
+    with every sample's age relative to the timed region's start."""
+    rec = {"settle_ms": settle_ms, "settle_launches": 0, "aligned_to_refresh": False}
+    per = max(per_launch_ms_hint, 1e-3)
+    sampling = False
+    if settle_ms > 0:
+        n, t0 = max(1, int(5.0 / per)), time.perf_counter()
+        while True:
+            ms = chunk(n)
+            rec["settle_launches"] += n
+            per = max(ms / n, 1e-3)
+            el = (time.perf_counter() - t0) * 1e3
+            if el >= settle_ms:
+                break
+            if not sampling and el >= min(300.0, settle_ms / 2):
+                sampling = clock.start(1000)
+            n = max(1, int(50.0 / per))
+        if sampling:
+            seen, t1 = clock.count(), time.perf_counter()
+            n = max(1, int(4.0 / per))
+            while clock.count() == seen and time.perf_counter() - t1 < 1.5:
+                chunk(n)
+                rec["settle_launches"] += n
+            rec["aligned_to_refresh"] = clock.count() > seen
+    else:
+        sampling = clock.start(1000)
+    t_start = clock.now_ms() if clock.ok else None
+    total = timed()
+    t_end = clock.now_ms() if clock.ok else None
+    samples = clock.samples() if sampling else []
+    if sampling:
+        clock.stop()
+    rec["timed_window_ms"] = round(t_end - t_start, 3) if t_start is not None else None
+    rec["samples"] = [{"age_ms": round(s.t_ms - t_start, 2), "sclk_mhz": round(s.gfx_mhz, 1),
+                       "socket_w": round(s.socket_w, 1), "gfx_busy_pct": round(s.gfx_activity, 1)}
+                      for s in samples]
+    rec["settle"] = _aggregate([s for s in samples if s.t_ms < t_start])
+    rec["timed"] = _aggregate([s for s in samples if t_start <= s.t_ms <= t_end])
+    rec["nearest"] = min(rec["samples"], key=lambda s: abs(s["age_ms"])) if samples else None
+    return total, rec
+
+
+def library_ceiling(A, B, out, args, cus, flop_clk_cu, peak, clock):
+    """torch.matmul on the same operands under measure()'s protocol, once per
+    BLAS backend torch offers on ROCm.  Comparison only."""
+    import torch
+    tdt = torch.float16 if out == "f16" else torch.float32
+    C2 = torch.empty((A.shape[0], B.shape[1]), dtype=tdt, device=A.device)
+    flop = 2.0 * A.shape[0] * B.shape[1] * A.shape[1]
+    bk = torch.backends.cuda
+    saved_backend = bk.preferred_blas_library()
+    saved_red = bk.matmul.allow_fp16_reduced_precision_reduction
+    bk.matmul.allow_fp16_reduced_precision_reduction = False  # fp32 accumulation throughout
+    res = {}
+    tuned = False
+    try:
+        if args.library_tune:
+            torch.cuda.tunable.enable(True)
+            torch.cuda.tunable.tuning_enable(True)
+            torch.cuda.tunable.set_filename(os.path.join(os.environ.get("TMPDIR", "/tmp"), "vk_tunableop.csv"))
+            tuned = True
+
+        def mm():
+            if out == "f16":
+                torch.matmul(A, B, out=C2)
+            else:
+                torch.mm(A, B, out_dtype=torch.float32, out=C2)
+
+        # torch's names on ROCm: "hipblaslt" (hipBLASLt), "hipblas" (rocBLAS
+        # through hipBLAS), "ck" (Composable Kernel GEMMs)
+        for name, backend in (("hipblaslt", "hipblaslt"), ("rocblas", "hipblas"), ("ck", "ck")):
+            try:
+                bk.preferred_blas_library(backend)
+            except Exception as e:  # noqa: BLE001 -- a backend this build lacks is reported, not fatal
+                res[name] = {"error": str(e)}
+                continue
+            try:
+                mm()
+                torch.cuda.synchronize()
+            except Exception as e:  # noqa: BLE001
+                res[name] = {"error": str(e)}
+                continue
+
+            def chunk(n):
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(n):
+                    mm()
+                e1.record()
+                e1.synchronize()
+                return e0.elapsed_time(e1)
+
+            def timed():
+                for _ in range(args.warmup):
+                    mm()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(args.steps):
+                    mm()
+                e1.record()
+                e1.synchronize()
+                torch.cuda.synchronize()
+                return e0.elapsed_time(e1)
+
+            C2.fill_(float("nan"))
+            total, rec = measure(clock, chunk, timed, args.settle_ms)
+            ms = total / args.steps
+            tf = flop / (ms * 1e-3) / 1e12
+            ok, max_abs, ratio = check_output(A, B, C2, out)
+            near = rec["nearest"]
+            sclk = near["sclk_mhz"] if near else None
+            pk = cus * flop_clk_cu * sclk * 1e6 / 1e12 if sclk else None
+            res[name] = {"ms_per_step": round(ms, 5), "tflops": round(tf, 2), "frac": round(tf / peak, 4),
+                         "sclk_mhz": sclk, "sclk_age_ms": near["age_ms"] if near else None,
+                         "frac_clock": round(tf / pk, 4) if pk else None,
+                         "output_within_bound": ok, "error_over_bound": round(ratio, 4), "clock": rec}
+    finally:
+        bk.preferred_blas_library(saved_backend)
+        bk.matmul.allow_fp16_reduced_precision_reduction = saved_red
+        if tuned:
+            torch.cuda.tunable.tuning_enable(False)
+            torch.cuda.tunable.enable(False)
+    timed_ok = {k: v for k, v in res.items() if "tflops" in v and v["output_within_bound"]}
+    best = max(timed_ok, key=lambda k: timed_ok[k]["tflops"]) if timed_ok else None
+    return {"best_backend": best,
+            "tflops": timed_ok[best]["tflops"] if best else None,
+            "ms_per_step": timed_ok[best]["ms_per_step"] if best else None,
+            "frac_clock": timed_ok[best]["frac_clock"] if best else None,
+            "tunableop": tuned,
+            "protocol": "torch.matmul on the same A, B (fp32 accumulation, allow_fp16_reduced_precision_"
+                        "reduction off), same settle length ending on a metrics refresh, same warm-up and "
+                        "steps back to back between one event pair; after the product's measurements",
+            "backends": res}
 
 
 def load_v0():
@@ -348,50 +548,38 @@ def main():
 
     clock = Clock(bench)
 
-    # Untimed settle phase: back-to-back launches until the clock has reached
-    # its sustained level (see --settle-ms); the clock is sampled after its
-    # first 300 ms.
-    settle_launches = 0
-    settle_clock = None
-    if args.settle_ms > 0:
-        # Chunks of back-to-back launches (about 50 ms each, sized from the
-        # previous chunk's event time) until the host clock says settle_ms
-        # have passed; the sampler runs from 300 ms on.
-        probe = ctypes.c_float(0.0)
-        chunk, sampling = 20, False
-        t0 = time.perf_counter()
-        while True:
-            st = bench.vkb_back_to_back(*call, chunk, ctypes.byref(probe))
-            if st != 0:
-                if sampling:
-                    clock.stop()
-                print(f"bench.py: settle phase failed with status {st}", file=sys.stderr)
-                return 1
-            settle_launches += chunk
-            el = (time.perf_counter() - t0) * 1e3
-            if el >= args.settle_ms:
-                break
-            if not sampling and el >= min(300.0, args.settle_ms / 2):
-                sampling = clock.start()
-            chunk = max(1, int(50.0 / max(probe.value / chunk, 1e-3)))
-        if sampling:
-            settle_clock = clock.stop()
+    # Settle phase and timed region (see measure()): the timed region is C++
+    # on the kernel's stream -- warm-up, device sync, `steps` launches back to
+    # back between one event pair, device sync.  Wall clock around it as a
+    # cross-check.
+    probe = ctypes.c_float(0.0)
 
-    # Timed region (C++, on the kernel's stream): warm-up, device sync, then
-    # `steps` launches back to back between one event pair, device sync.
-    # Wall clock around it as a cross-check; the clock sampled throughout.
+    def chunk(n):
+        st = bench.vkb_back_to_back(*call, n, ctypes.byref(probe))
+        if st != 0:
+            raise RuntimeError(f"settle phase failed with status {st}")
+        return probe.value
+
     tot = ctypes.c_float(0.0)
-    torch.cuda.synchronize()
-    sampling = clock.start()
-    w0 = time.perf_counter()
-    st = bench.vkb_stream_loop(*call, args.warmup, args.steps, ctypes.byref(tot))
-    torch.cuda.synchronize()
-    wall = time.perf_counter() - w0
-    timed_clock = clock.stop() if sampling else None
-    if st != 0:
-        print(f"bench.py: timed loop failed with status {st}", file=sys.stderr)
+    wall = [0.0]
+
+    def timed():
+        torch.cuda.synchronize()
+        w0 = time.perf_counter()
+        st = bench.vkb_stream_loop(*call, args.warmup, args.steps, ctypes.byref(tot))
+        torch.cuda.synchronize()
+        wall[0] = time.perf_counter() - w0
+        if st != 0:
+            raise RuntimeError(f"timed loop failed with status {st}")
+        return tot.value
+
+    try:
+        total_ms, clock_rec = measure(clock, chunk, timed, args.settle_ms)
+    except RuntimeError as e:
+        print(f"bench.py: {e}", file=sys.stderr)
         return 1
-    mean_ms = tot.value / args.steps
+    wall = wall[0]
+    mean_ms = total_ms / args.steps
     flop = 2.0 * m * n * k
     tflops = flop / (mean_ms * 1e-3) / 1e12
 
@@ -427,13 +615,10 @@ def main():
     # FLOP per clock per CU: dense fp16 MFMA 4096; fp32 (vector FMA or fp32
     # MFMA) 256.  The peak at the measured SCLK is what the clock allowed.
     flop_clk_cu = 4096 if dtype == "f16" else 256
-    sclk_src = None
-    if timed_clock and timed_clock["samples"] >= 3:
-        sclk, sclk_src = timed_clock["sclk_mhz"], "timed region"
-    elif settle_clock:
-        sclk, sclk_src = settle_clock["sclk_mhz"], "settle phase (same call back to back, after its first 300 ms)"
-    else:
-        sclk = None
+    near = clock_rec["nearest"]
+    sclk = near["sclk_mhz"] if near else None
+    sclk_src = (f"the metrics sample nearest the timed region's start (age {near['age_ms']} ms; "
+                f"negative: before the start)") if near else None
     peak_at_sclk = cus * flop_clk_cu * sclk * 1e6 / 1e12 if sclk else None
     workload = f"gemm_{dtype}_{m}x{n}x{k}"
     esz = 2 if dtype == "f16" else 4
@@ -495,16 +680,21 @@ def main():
         },
         "pct_of_peak": round(100.0 * tflops / peak, 2),
         "wall_ms_per_step": round(wall * 1e3 / (args.steps + args.warmup), 5),
-        "settle": {"ms": args.settle_ms, "launches": settle_launches,
+        "settle": {"ms": args.settle_ms, "launches": clock_rec["settle_launches"],
+                   "ends_on_metrics_refresh": clock_rec["aligned_to_refresh"],
                    "note": "the timed dispatches are launches settle.launches + warmup .. + steps - 1 of the run"},
         "reference_loop": ref_loop,
         "clock": {
-            "timed": timed_clock,
-            "settle": settle_clock,
+            "timed": clock_rec["timed"],
+            "settle": clock_rec["settle"],
+            "samples": clock_rec["samples"],
+            "nearest": near,
+            "timed_window_ms": clock_rec["timed_window_ms"],
             "sclk_for_frac_clock": sclk_src,
             "source": "amd-smi gpu_metrics (current_gfxclks averaged over XCDs, current_uclk, "
-                      "current_socket_power, average_gfx_activity) polled every 2 ms on a host thread; "
-                      "the table refreshes about once per second",
+                      "current_socket_power, average_gfx_activity) polled every 1 ms on a host thread; "
+                      "the table refreshes about once per second; age_ms = host time of the read that "
+                      "saw a refresh minus the timed region's start",
             "error": clock.error,
         },
         "device": {"name": props.name, "cus": cus, "host_cores": os.cpu_count(),
@@ -514,6 +704,13 @@ def main():
         "reference_best_a100_frac_of_peak": 0.897,
         "roofline": roofline,
     }
+    if not args.no_library_ceiling and dtype == "f16":
+        lib_ceiling = library_ceiling(A, B, out, args, cus, flop_clk_cu, peak, clock)
+        if lib_ceiling["tflops"]:
+            lib_ceiling["product_over_library"] = round(tflops / lib_ceiling["tflops"], 4)
+        res["library_ceiling"] = lib_ceiling
+    else:
+        res["library_ceiling"] = None
     if not args.no_cpu_baseline:
         res["cpu_baseline"] = cpu_baseline(m, n, k, dtype, args.seed, args.cpu_seconds)
     else:

@@ -62,6 +62,15 @@ typedef struct vkb_clock_stats {
   double gfx_activity_mean; /* GFX busy percentage (-1: not reported) */
 } vkb_clock_stats;
 
+/* One refresh of the metrics table seen by the sampler. */
+typedef struct vkb_clock_sample {
+  double t_ms;          /* host steady-clock time (CLOCK_MONOTONIC, ms) of the read that saw the refresh */
+  double gfx_mhz;       /* SCLK, mean over XCDs */
+  double uclk_mhz;      /* memory clock (0: not reported) */
+  double socket_w;      /* socket power in W (0: not reported) */
+  double gfx_activity;  /* GFX busy percentage (-1: not reported) */
+} vkb_clock_sample;
+
 /* Open the sampler for the current HIP device (VK_OK, or VK_ERR_HIP with the
  * reason in vkb_clock_error()). */
 int vkb_clock_open(void);
@@ -70,6 +79,13 @@ int vkb_clock_start(int interval_us);
 /* Stop and fill *out; VK_ERR_HIP when no sample was taken. */
 int vkb_clock_stop(vkb_clock_stats* out);
 const char* vkb_clock_error(void);
+/* The refreshes seen so far in the current (or last) region, oldest first:
+ * copies up to `max` into out (may be NULL) and returns how many there are.
+ * Safe to call while sampling. */
+int vkb_clock_samples(vkb_clock_sample* out, int max);
+/* The sampler's time base now (CLOCK_MONOTONIC, ms), to place a region's
+ * start among the samples. */
+double vkb_clock_now_ms(void);
 
 #ifdef __cplusplus
 }

@@ -66,6 +66,10 @@ struct Sampler {
     int busy_n = 0;
     uint64_t last_ts = 0;
     bool primed = false;  // the table as the region began has been read
+    // Every refresh seen in the region, with the host time of the read that
+    // saw it; guarded by dmu (read by vkb_clock_samples while sampling).
+    std::mutex dmu;
+    std::vector<vkb_clock_sample> log;
     std::chrono::steady_clock::time_point t0;
     double window_ms = 0;
 
@@ -158,6 +162,18 @@ struct Sampler {
         }
         if (n == 0) return;
         const double g = s / n;
+        vkb_clock_sample rec{};
+        rec.t_ms = std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch())
+                       .count();
+        rec.gfx_mhz = g;
+        rec.uclk_mhz = (m.current_uclk != 0 && m.current_uclk != 0xffff) ? m.current_uclk : 0.0;
+        rec.socket_w = (m.current_socket_power != 0 && m.current_socket_power != 0xffff) ? m.current_socket_power
+                                                                                          : 0.0;
+        rec.gfx_activity = m.average_gfx_activity != 0xffff ? m.average_gfx_activity : -1.0;
+        {
+            std::lock_guard<std::mutex> lk(dmu);
+            log.push_back(rec);
+        }
         samples++;
         gfx_sum += g;
         gfx_min = std::fmin(gfx_min, g);
@@ -221,6 +237,10 @@ extern "C" int vkb_clock_start(int interval_us) {
     s.busy_n = 0;
     s.last_ts = 0;
     s.primed = false;
+    {
+        std::lock_guard<std::mutex> dl(s.dmu);
+        s.log.clear();
+    }
     s.stop.store(false);
     s.t0 = std::chrono::steady_clock::now();
     s.th = std::thread([&s] { s.loop(); });
@@ -250,4 +270,17 @@ extern "C" int vkb_clock_stop(vkb_clock_stats* out) {
         out->gfx_activity_mean = s.busy_n ? s.busy_sum / s.busy_n : -1.0;
     }
     return s.samples ? VK_OK : VK_ERR_HIP;
+}
+
+extern "C" double vkb_clock_now_ms(void) {
+    return std::chrono::duration<double, std::milli>(std::chrono::steady_clock::now().time_since_epoch()).count();
+}
+
+extern "C" int vkb_clock_samples(vkb_clock_sample* out, int max) {
+    Sampler& s = sampler();
+    std::lock_guard<std::mutex> lk(s.dmu);
+    const int n = (int)s.log.size();
+    if (out)
+        for (int i = 0; i < n && i < max; i++) out[i] = s.log[i];
+    return n;
 }
