@@ -138,7 +138,15 @@ const char* vk_gemm_name(int version, vk_dtype in_dtype);
 int vk_gemm_query(int version, vk_dtype in_dtype, vk_caps* caps);
 
 /* Write up to max_count version ids for in_dtype into out; return how many
- * exist. */
+ * exist.  fp16 versions VK_F16_LEAVE_ONE_OUT_FIRST .. _LAST are version 7
+ * with one ingredient of its k-loop or tile order turned off each (71: A
+ * swizzle, 72: B swizzle, 73: direct-to-LDS loads replaced by VGPR staging,
+ * 74: B ring cut to 2 slots, 75: no ping-pong, 76: no XCD-aware tile order,
+ * 77: no accumulator chains of 2); they exist to be measured against
+ * version 7 (bitwise equal results, same shapes accepted) and have no
+ * counterpart in the reference. */
+#define VK_F16_LEAVE_ONE_OUT_FIRST 71
+#define VK_F16_LEAVE_ONE_OUT_LAST 77
 int vk_gemm_list(vk_dtype in_dtype, int* out, int max_count);
 
 /* Check a call without launching: the same validation vk_gemm performs. */

@@ -161,6 +161,11 @@ def abi_version() -> int:
     return int(load().vk_gemm_abi_version())
 
 
+# fp16 versions 71-77: version 7 with one ingredient turned off each
+# (include/vk_gemm.h, VK_F16_LEAVE_ONE_OUT_FIRST/_LAST); measured, never picked.
+LEAVE_ONE_OUT = range(71, 78)
+
+
 def versions(in_dtype: int) -> list:
     L = load()
     n = L.vk_gemm_list(in_dtype, None, 0)

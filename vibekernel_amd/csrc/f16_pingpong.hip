@@ -567,6 +567,25 @@ using pp64::kLdsBytes;
 __host__ __device__ constexpr int swz_a16(int row) { return (row >> 1) & 7; }
 __host__ __device__ constexpr int swz_b16(int krow) { return swz_b(krow) ^ (((krow >> 3) & 1) << 1); }
 
+// Leave-one-out instances of version 7 (versions 71-77): each turns off one
+// ingredient of the k-loop or the tile order and keeps everything else, so
+// that a kernel trace and counters show what that ingredient buys.  All of
+// them compute every element in the same order as version 7 (bitwise equal
+// results); none is ever picked.
+constexpr int kAblNoSwzA = 1;      // A k-tile rows stored unswizzled (chunk c at slot c)
+constexpr int kAblNoSwzB = 2;      // B k-rows stored unswizzled
+constexpr int kAblRegStage = 4;    // global -> VGPR -> ds_write_b128 instead of direct-to-LDS loads
+constexpr int kAblB2 = 8;          // B ring of 2 slots: B(t+1) loaded during compute(t) (prefetch 1 ahead)
+constexpr int kAblNoPingPong = 16; // both groups in phase: all 8 waves read, then all compute
+constexpr int kAblNoXcd = 32;      // grouped raster without the XCD remap
+constexpr int kAblNoChain = 64;    // MFMAs rotate over the 32 accumulators (k-step 0 of all, then 1)
+
+template <int kAbl>
+constexpr int lds_bytes_of() {
+  return (kAbl & kAblB2) ? kBOff + 2 * kBBytes : kLdsBytes;
+}
+static_assert(lds_bytes_of<kAblB2>() >= 8 * 128 * 64 * 2, "fp16 epilogue staging: 16 KB per wave");
+
 // Store of a wave's 128x64 block of C through its 16 KB LDS staging region,
 // in two halves of 64 rows: stage() the 16 MFMA blocks (i, j) of a half, then
 // flush() it.  Block (i, j), register r, lane l holds
@@ -675,10 +694,19 @@ __device__ __forceinline__ void epilogue16_edge(float4v (&acc)[8][4], uint32_t w
 // idle.  A and B point at the whole matrices; m0, n0 name the tile.  kEdge
 // (version 10): the tile may reach past M rows, N columns or K (M any; N, K
 // multiples of 8); what lies outside the matrices is loaded as zeros.
-template <bool kEdge = false>
+//
+// kAbl (versions 71-77, whole tiles only): the kAbl* ingredients turned off.
+template <bool kEdge = false, int kAbl = 0>
 __device__ __forceinline__ void pp16_mainloop(const half_t* __restrict__ A, const half_t* __restrict__ B, int N,
                                               int K, int m0, int n0, int kb, int nk, uint32_t lds_base, int grp,
                                               int gw, int lane, float4v (&acc)[8][4], int M = 0) {
+  static_assert(!(kEdge && kAbl), "the leave-one-out instances take whole tiles only");
+  constexpr bool kSwzA = !(kAbl & kAblNoSwzA), kSwzB = !(kAbl & kAblNoSwzB);
+  constexpr bool kDma = !(kAbl & kAblRegStage), kPP = !(kAbl & kAblNoPingPong);
+  constexpr bool kB2 = kAbl & kAblB2, kChain = !(kAbl & kAblNoChain);
+  constexpr int kNB = kB2 ? 2 : kBSlots;  // B slots
+  auto sa = [](int row) { return kSwzA ? swz_a16(row) : 0; };
+  auto sb = [](int krow) { return kSwzB ? swz_b16(krow) : 0; };
   // ---- direct-to-LDS duty: instruction d = 4h + i (8 per wave per k-tile) ----
   // Q, A: rows gw*32 + 8i .. +7 of the A-top (h = 0) or A-bot (h = 1) half,
   //   landing at half offset (gw*4 + i) * 1024.
@@ -690,11 +718,11 @@ __device__ __forceinline__ void pp16_mainloop(const half_t* __restrict__ A, cons
   for (int i = 0; i < 4; i++) {
     if (grp) {
       const int row = gw * 32 + i * 8 + (lane >> 3);
-      const int c = (lane & 7) ^ swz_a16(row);
+      const int c = (lane & 7) ^ sa(row);
       voff[i] = (uint32_t)(((size_t)row * K + c * 8) * 2);
     } else {
       const int krow = gw * 16 + 2 * (i & 1) + 8 * (i >> 1) + (lane >> 5);
-      const int c = (lane & 31) ^ swz_b16(krow);
+      const int c = (lane & 31) ^ sb(krow);
       voff[i] = (uint32_t)(((size_t)krow * N + c * 8) * 2);
     }
   }
@@ -724,7 +752,7 @@ __device__ __forceinline__ void pp16_mainloop(const half_t* __restrict__ A, cons
 #pragma unroll
       for (int i = 0; i < 4; i++) {
         const int row = gw * 32 + i * 8 + (lane >> 3);
-        akin |= (uint32_t)(((lane & 7) ^ swz_a16(row)) * 8) << (6 * i);
+        akin |= (uint32_t)(((lane & 7) ^ sa(row)) * 8) << (6 * i);
       }
     }
   }
@@ -787,6 +815,29 @@ __device__ __forceinline__ void pp16_mainloop(const half_t* __restrict__ A, cons
     }
   };
   auto dma = [&](int d, int kt, int slot) { dma_with(d, dma_ops(kt, slot)); };
+  // kAblRegStage: the same 16 bytes per lane through a VGPR and a ds_write
+  // to the address the direct-to-LDS load would have filled.
+  const uint32_t lane16 = (uint32_t)lane * 16;
+  auto gload = [&](int d, const DmaOps& o) -> uint4v {
+    return *reinterpret_cast<const uint4v*>(o.g[d >> 2] + voff[d & 3]);
+  };
+  auto swrite = [&](int d, const DmaOps& o, const uint4v& v) {
+    lds_write16(o.l[d] + lane16, __builtin_bit_cast(float4v, v));
+  };
+  // All 8 loads of one k-tile, written as they land (prologue).
+  auto stage_tile = [&](int kt, int slot) {
+    if constexpr (kDma) {
+#pragma unroll
+      for (int d = 0; d < 8; d++) dma(d, kt, slot);
+    } else {
+      const DmaOps o = dma_ops(kt, slot);
+      uint4v v[8];
+#pragma unroll
+      for (int d = 0; d < 8; d++) v[d] = gload(d, o);
+#pragma unroll
+      for (int d = 0; d < 8; d++) swrite(d, o, v[d]);
+    }
+  };
 
   // ---- fragment addresses ----
   // A block i, k-step s: half-row i*16 + l%16, chunk 4s + l/16.
@@ -795,7 +846,7 @@ __device__ __forceinline__ void pp16_mainloop(const half_t* __restrict__ A, cons
   uint32_t aoff[2];
 #pragma unroll
   for (int s2 = 0; s2 < 2; s2++)
-    aoff[s2] = a_half + arow * (kBK * 2) + 16 * ((4 * s2 + (lane >> 4)) ^ swz_a16(arow));
+    aoff[s2] = a_half + arow * (kBK * 2) + 16 * ((4 * s2 + (lane >> 4)) ^ sa(arow));
   // B block j, k-step s, half h: lane 16g + 4jj + q names k-row
   // 32s + 8g + 4h + jj, columns gw*64 + 16j + 4q .. +3; the transpose read
   // hands lane 16g + c the 4 k of column 16j + c.
@@ -805,7 +856,7 @@ __device__ __forceinline__ void pp16_mainloop(const half_t* __restrict__ A, cons
 #pragma unroll
   for (int j = 0; j < 4; j++) {
     const int c = gw * 8 + 2 * j + (q >> 1);
-    boff[j] = kBOff + krow0 * (kBN * 2) + 16 * (c ^ swz_b16(krow0)) + 8 * (q & 1);
+    boff[j] = kBOff + krow0 * (kBN * 2) + 16 * (c ^ sb(krow0)) + 8 * (q & 1);
   }
 
 #pragma unroll
@@ -850,57 +901,96 @@ __device__ __forceinline__ void pp16_mainloop(const half_t* __restrict__ A, cons
   // sustained clock by ~4% over rotating through the accumulators, at the
   // same issue rate.  Per element the sum order (k-step 0, then 1) is
   // unchanged.  The scheduling barriers keep the pairs adjacent.
+  // Load d of the k-tile described by `o`: direct-to-LDS, or (kAblRegStage)
+  // into stg[d], written to LDS four loads later (the compiler waits for
+  // that load alone: vmcnt(3)), the last four after the MFMAs.
+  uint4v stg[8];
+  auto load_step = [&](int d, const DmaOps& o) {
+    if constexpr (kDma) {
+      dma_with(d, o);
+    } else {
+      if (d >= 4) swrite(d - 4, o, stg[d - 4]);
+      stg[d] = gload(d, o);
+    }
+  };
   auto compute_and_load = [&](const DmaOps& o) {
+    if constexpr (kChain) {
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
+      for (int i = 0; i < 8; i++) {
 #pragma unroll
-      for (int j = 0; j < 4; j++) {
-        acc[i][j] = mfma16x16x32(fb[0][j], fa[0][i], acc[i][j]);
-        __builtin_amdgcn_sched_barrier(0);
-        acc[i][j] = mfma16x16x32(fb[1][j], fa[1][i], acc[i][j]);
+        for (int j = 0; j < 4; j++) {
+          acc[i][j] = mfma16x16x32(fb[0][j], fa[0][i], acc[i][j]);
+          __builtin_amdgcn_sched_barrier(0);
+          acc[i][j] = mfma16x16x32(fb[1][j], fa[1][i], acc[i][j]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        load_step(i, o);
         __builtin_amdgcn_sched_barrier(0);
       }
-      dma_with(i, o);
+    } else {
+#pragma unroll
+      for (int s2 = 0; s2 < 2; s2++)
+#pragma unroll
+        for (int i = 0; i < 8; i++) {
+#pragma unroll
+          for (int j = 0; j < 4; j++) {
+            acc[i][j] = mfma16x16x32(fb[s2][j], fa[s2][i], acc[i][j]);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+          if (i & 1) {
+            load_step(4 * s2 + (i >> 1), o);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+    }
+    if constexpr (!kDma) {
+#pragma unroll
+      for (int d = 4; d < 8; d++) swrite(d, o, stg[d]);
       __builtin_amdgcn_sched_barrier(0);
     }
   };
 
-  // Prologue and loop: exactly as version 6.
+  // Prologue and loop: exactly as version 6.  kAblB2: P keeps B one k-tile
+  // ahead (B(t+1) in compute(t), waited for at its end); kAblNoPingPong: no
+  // extra barrier for Q at the start or for P at the end, and every wave
+  // waits for k-tile t+1 after compute(t).
   const int kt1 = min(1, nk - 1);
-#pragma unroll
-  for (int d = 0; d < 8; d++) dma(d, 0, 0);
-#pragma unroll
-  for (int d = 0; d < 8; d++) dma(d, kt1, 1);
+  stage_tile(0, 0);
+  if (!kB2 || grp) stage_tile(kt1, 1);
   if (grp)
-    wait_vmcnt<12>();
+    wait_vmcnt<kPP ? 12 : 8>();
   else
-    wait_vmcnt<8>();
+    wait_vmcnt<kB2 ? 0 : 8>();
   lds_barrier();
-  if (grp) {
+  if (kPP && grp) {
     wait_vmcnt<8>();
     lds_barrier();
   }
 
   for (int t = 0; t < nk; t++) {
     const int aslot = t & 1;
-    const int bslot = t % kBSlots;
+    const int bslot = t % kNB;
     const int kt2 = min(t + 2, nk - 1);
+    const int ktp = kB2 && !grp ? min(t + 1, nk - 1) : kt2;  // this wave's loads
     __builtin_amdgcn_sched_barrier(0);
     read_frags(aslot, bslot);
     __builtin_amdgcn_sched_barrier(0);  // the reads go out first
-    const DmaOps ops = dma_ops(kt2, grp ? aslot : (t + 2) % kBSlots);
+    const DmaOps ops = dma_ops(ktp, grp ? aslot : (t + (kB2 ? 1 : 2)) % kNB);
     pin_ops(ops);
-    if (grp) wait_vmcnt<4>();  // Q: A-top(t+1) landed before barrier 2t+2
+    if (kPP && grp) wait_vmcnt<4>();  // Q: A-top(t+1) landed before barrier 2t+2
     __builtin_amdgcn_sched_barrier(0);
     lds_barrier();
     __builtin_amdgcn_sched_barrier(0);
     compute_and_load(ops);
-    wait_vmcnt<8>();  // P: B(t+1); Q: A-top(t+1), A-bot(t+1)
+    if (kB2 && !grp)
+      wait_vmcnt<0>();  // P: B(t+1)
+    else
+      wait_vmcnt<8>();  // P: B(t+1); Q: A-top(t+1), A-bot(t+1)
     __builtin_amdgcn_sched_barrier(0);
     lds_barrier();
   }
   __builtin_amdgcn_sched_barrier(0);
-  if (!grp) lds_barrier();
+  if (kPP && !grp) lds_barrier();
   wait_vmcnt<0>();
   lds_barrier();
 }
@@ -947,6 +1037,49 @@ hipError_t launch_t(const GemmArgs& a) {
 
 hipError_t launch(const GemmArgs& a) {
   return a.out_dtype == VK_DTYPE_F16 ? launch_t<half_t>(a) : launch_t<float>(a);
+}
+
+// Versions 71-77: version 7 with one ingredient off (kAbl, see kAblNoSwzA).
+template <typename OutT, int kAbl>
+__global__ __launch_bounds__(kThreads) void f16_pp16_abl_kernel(const half_t* __restrict__ A,
+                                                                const half_t* __restrict__ B,
+                                                                OutT* __restrict__ C, int M, int N, int K) {
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int grp = wave >> 2;
+  const int gw = wave & 3;
+
+  int tm, tn;
+  if constexpr ((kAbl & kAblNoXcd) != 0)
+    raster_tile(blockIdx.x, M / kBM, N / kBN, tm, tn);
+  else
+    tile_of(blockIdx.x, M / kBM, N / kBN, tm, tn);
+  const int m0 = tm * kBM, n0 = tn * kBN;
+  const uint32_t lds_base = lds_addr32(lds);
+
+  float4v acc[8][4];
+  pp16_mainloop<false, kAbl>(A, B, N, K, m0, n0, 0, K / kBK, lds_base, grp, gw, lane, acc);
+  epilogue16<OutT>(acc, lds_base + wave * (128 * 64 * 2), C + (size_t)(m0 + grp * 128) * N + n0 + gw * 64, N,
+                   lane_from_exec());
+}
+
+template <typename OutT, int kAbl>
+hipError_t launch_abl_t(const GemmArgs& a) {
+  static std::atomic<uint64_t> attr_done{0};
+  auto kfn = f16_pp16_abl_kernel<OutT, kAbl>;
+  hipError_t e = ensure_lds_attr(kfn, lds_bytes_of<kAbl>(), a.device, attr_done);
+  if (e != hipSuccess) return e;
+  const int tiles = (int)((a.m / kBM) * (a.n / kBN));
+  hipLaunchKernelGGL(kfn, dim3(tiles), dim3(kThreads), lds_bytes_of<kAbl>(), a.stream,
+                     static_cast<const half_t*>(a.A), static_cast<const half_t*>(a.B),
+                     static_cast<OutT*>(a.C), (int)a.m, (int)a.n, (int)a.k);
+  return hipGetLastError();
+}
+
+template <int kAbl>
+hipError_t launch_abl(const GemmArgs& a) {
+  return a.out_dtype == VK_DTYPE_F16 ? launch_abl_t<half_t, kAbl>(a) : launch_abl_t<float, kAbl>(a);
 }
 
 // ---------------------------------------------------------------------------
@@ -1221,6 +1354,32 @@ void register_f16_pingpong() {
   e7.caps.version = 7;
   e7.launch = pp16::launch;
   register_kernel(e7);
+
+  // Leave-one-out instances of version 7 (never picked; bench.py --version N).
+  struct Abl {
+    int version;
+    const char* name;
+    LaunchFn launch;
+    int lds;
+  };
+  const Abl abl[] = {
+      {71, "f16_v71_v7_no_swizzle_a", pp16::launch_abl<pp16::kAblNoSwzA>, pp64::kLdsBytes},
+      {72, "f16_v72_v7_no_swizzle_b", pp16::launch_abl<pp16::kAblNoSwzB>, pp64::kLdsBytes},
+      {73, "f16_v73_v7_vgpr_staging", pp16::launch_abl<pp16::kAblRegStage>, pp64::kLdsBytes},
+      {74, "f16_v74_v7_b_ring2", pp16::launch_abl<pp16::kAblB2>, pp16::lds_bytes_of<pp16::kAblB2>()},
+      {75, "f16_v75_v7_no_pingpong", pp16::launch_abl<pp16::kAblNoPingPong>, pp64::kLdsBytes},
+      {76, "f16_v76_v7_no_xcd_order", pp16::launch_abl<pp16::kAblNoXcd>, pp64::kLdsBytes},
+      {77, "f16_v77_v7_no_mfma_chain", pp16::launch_abl<pp16::kAblNoChain>, pp64::kLdsBytes},
+  };
+  for (const Abl& x : abl) {
+    KernelEntry ea = e7;
+    ea.version = x.version;
+    ea.name = x.name;
+    ea.caps.version = x.version;
+    ea.caps.lds_bytes = x.lds;
+    ea.launch = x.launch;
+    register_kernel(ea);
+  }
 
   KernelEntry e10 = e7;
   e10.version = 10;

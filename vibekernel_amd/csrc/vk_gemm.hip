@@ -31,7 +31,7 @@ namespace vk {
 namespace {
 
 // The registered versions, in a fixed array: a lookup never allocates.
-constexpr int kMaxEntries = 32;
+constexpr int kMaxEntries = 48;
 struct Registry {
   KernelEntry e[kMaxEntries];
   int n = 0;
