@@ -1,0 +1,119 @@
+"""The gfx950 LDS bank model behind the kernels' LDS layouts, pinned on
+measurements, and the layouts checked against it (CPU only).
+
+Measured on MI355X with tests/golden/lds_bank_probe.hip (one wave, 16
+instances of one LDS instruction per dispatch, SQ_LDS_BANK_CONFLICT under
+rocprofv3; fixture tests/golden/lds_bank_probe_gfx950.json):
+
+* the banks are 64 x 4 bytes: two accesses conflict when their addresses
+  differ by a multiple of 256 bytes (for 16-byte accesses: the same 16-byte
+  slot, address / 16 mod 16), and only if the hardware serves them in the
+  same pass;
+* ds_read_b128 is served in 4 passes of 16 lanes: lane l is in pass
+  (l / 32, parity of bits 2-4 of l) -- not 16 consecutive lanes;
+* ds_read_b64 in 2 passes of 32 consecutive lanes, ds_write_b128 in 8
+  passes of 8, ds_write_b64 in 4 passes of 16;
+* a pass costs one cycle per distinct address on its most-used slot.
+
+The probe's two-lane patterns fix the pass of every lane; its whole-wave
+patterns (the kernels' own fragment reads) check the cycle count.  Under
+this model version 8's A fragment reads with chunk ^ (row / 4) % 4 take 8
+cycles instead of 4 (the 25-33 % conflict share its counters showed), and
+chunk ^ (row / 2) % 4, the kernel's layout, takes 4."""
+import json
+import os
+import re
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+FIXTURE = os.path.join(ROOT, "tests", "golden", "lds_bank_probe_gfx950.json")
+
+import sys  # noqa: E402
+sys.path.insert(0, os.path.join(ROOT, "tests", "golden"))
+import make_lds_bank_fixture as pat  # noqa: E402
+
+
+def _parity(x):
+    return bin(x).count("1") & 1
+
+
+PASS_OF = {
+    "rd128": lambda l: (l >> 5, _parity((l >> 2) & 7)),
+    "rd64": lambda l: l >> 5,
+    "wr128": lambda l: l >> 3,
+    "wr64": lambda l: l >> 4,
+}
+SLOT_BYTES = {"rd128": 16, "rd64": 8, "wr128": 16, "wr64": 8}
+
+
+def conflict_cycles(op, addrs, lanes=range(64)):
+    """Cycles beyond one per pass: in each pass, the distinct addresses on
+    its most-used slot (address mod 256 in SLOT_BYTES units), minus one."""
+    sb = SLOT_BYTES[op]
+    passes = {}
+    for l in lanes:
+        passes.setdefault(PASS_OF[op](l), {}).setdefault((addrs[l] % 256) // sb, set()).add(addrs[l] // sb)
+    return sum(max(len(v) for v in slots.values()) - 1 for slots in passes.values())
+
+
+@pytest.fixture(scope="module")
+def probe():
+    return json.load(open(FIXTURE))
+
+
+@pytest.mark.parametrize("op", ["rd128", "rd64", "wr128", "wr64"])
+def test_pass_model_matches_every_measured_lane_pair(probe, op):
+    pairs = probe["pairs_" + op]
+    assert len(pairs) == 249
+    for a, b, conf in pairs:
+        addrs = [0] * 64
+        addrs[b] = 256
+        assert conflict_cycles(op, addrs, lanes=(a, b)) == conf, (op, a, b, conf)
+
+
+def test_rd128_model_matches_whole_wave_patterns(probe):
+    funcs = {"rd128 v7A s2=0": lambda l: pat.v7_a(l, 0), "rd128 v7A s2=1": lambda l: pat.v7_a(l, 1),
+             "rd128 v7flush q=0": lambda l: pat.v7_flush(l, 0), "rd128 v7flush q=1": lambda l: pat.v7_flush(l, 1),
+             "rd128 linear": lambda l: 16 * l}
+    for name, f in pat.V8_SWIZZLES.items():
+        funcs[f"rd128 v8A {name}"] = lambda l, f=f: pat.v8_a(l, f)
+    measured = {p[0]: (p[1], p[2]) for p in probe["patterns"]}
+    for label, f in funcs.items():
+        conf, active = measured[label]
+        assert active == 4 + conf, label  # 4 passes plus the conflict cycles
+        assert conflict_cycles("rd128", [f(l) for l in range(64)]) == conf, label
+
+
+def test_consecutive_lane_passes_would_not_explain_the_measurements(probe):
+    """The obvious model (passes of 16 consecutive lanes) calls version 8's
+    old A layout conflict-free, which the probe contradicts: the pass
+    structure above is what the layouts must be designed against."""
+    measured = {p[0]: p[1] for p in probe["patterns"]}
+    old = [pat.v8_a(l, pat.V8_SWIZZLES["swz(row>>2)&3"]) for l in range(64)]
+    naive = {}
+    for l in range(64):
+        naive.setdefault(l >> 4, {}).setdefault((old[l] % 256) // 16, set()).add(old[l] // 16)
+    assert sum(max(len(v) for v in s.values()) - 1 for s in naive.values()) == 0
+    assert measured["rd128 v8A swz(row>>2)&3"] == 4
+
+
+def _v8_swizzle_shift():
+    src = open(os.path.join(ROOT, "vibekernel_amd", "csrc", "f16_skinny_sk.hip")).read()
+    m = re.search(r"constexpr int swz_a64\(int row\) \{ return \(row >> (\d)\) & 3; \}", src)
+    assert m, "swz_a64 not found in f16_skinny_sk.hip"
+    return int(m.group(1))
+
+
+def test_version8_a_reads_conflict_free_and_loads_whole_rows():
+    shift = _v8_swizzle_shift()
+    swz = lambda r: (r >> shift) & 3  # noqa: E731
+    assert conflict_cycles("rd128", [pat.v8_a(l, swz) for l in range(64)]) == 0
+    # the layout the kernel had before fails the model: 4 conflict cycles per read
+    assert conflict_cycles("rd128", [pat.v8_a(l, pat.V8_SWIZZLES["swz(row>>2)&3"]) for l in range(64)]) == 4
+    # The direct-to-LDS load of a 16-row A block stays one 1 KB row of the
+    # block per instruction: lane l lands at row l / 4, slot l % 4 and
+    # fetches chunk (l % 4) ^ swz(row) of that row, so every row's 4 lanes
+    # fetch its 64 contiguous global bytes.
+    for row in range(16):
+        assert sorted(((l & 3) ^ swz(row)) for l in range(4 * row, 4 * row + 4)) == [0, 1, 2, 3]

@@ -170,6 +170,27 @@ __global__ __launch_bounds__(256) void f32_valu_kernel(const float* __restrict__
   "v236", "v237", "v238", "v239", "v240", "v241", "v242", "v243", "v244", "v245", "v246", "v247", "v248", \
   "v249", "v250", "v251", "v252", "v253", "v254", "v255"
 
+// Tile order of the asm kernel (a 1-D grid): workgroups are dealt round-robin
+// over the 8 XCDs (workgroup b runs on XCD b % 8), so XCD x gets raster
+// positions [x T / 8, (x + 1) T / 8) when 8 divides the tile count T; the
+// raster walks 8 row panels at a time, column strip by column strip, so an
+// XCD's share is a block of 8 row panels x T / 64 column strips (at 4096^3:
+// 8 x 8 tiles, 16 MB of A panels and 32 MB of B strips per XCD, where the
+// row-major 2-D grid gave each XCD all 32 A panels and 2 B strips).
+__host__ __device__ __forceinline__ void f32_tile_of(uint32_t bid, uint32_t tiles_m, uint32_t tiles_n, uint32_t& tm,
+                                                     uint32_t& tn) {
+  constexpr uint32_t GM = 8;
+  const uint32_t total = tiles_m * tiles_n;
+  const uint32_t cid = (total & 7) == 0 ? (bid & 7) * (total >> 3) + (bid >> 3) : bid;
+  const uint32_t group = GM * tiles_n;
+  const uint32_t g = cid / group;
+  const uint32_t first_m = g * GM;
+  const uint32_t gm = tiles_m - first_m < GM ? tiles_m - first_m : GM;
+  const uint32_t r = cid - g * group;
+  tm = first_m + r % gm;
+  tn = r / gm;
+}
+
 // The asm kernel's 32-bit byte offsets: A's 128-row panel, B's 256-column
 // strip over all of K, and C's 128-row panel.
 bool asm_offsets_fit(size_t m, size_t n, size_t k) {
@@ -218,13 +239,15 @@ bool asm_offsets_fit(size_t m, size_t n, size_t k) {
 // sums, bit for bit, as the C++ kernel and the oracle.
 __global__ __launch_bounds__(256) void f32_valu_asm_kernel(const float* __restrict__ A,
                                                            const float* __restrict__ B, float* __restrict__ C,
-                                                           int N, int K) {
+                                                           int M, int N, int K) {
   __shared__ __attribute__((aligned(1024))) float As[2][kTM * kBK];
   __shared__ __attribute__((aligned(1024))) float Bs[2][kBK * kTN];
   const uint32_t tid = threadIdx.x;
   const uint32_t tx = tid & 15, ty = tid >> 4, lane = tid & 63;
   const uint32_t w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const size_t m0 = (size_t)blockIdx.y * kTM, n0 = (size_t)blockIdx.x * kTN;
+  uint32_t tm, tn;
+  f32_tile_of(blockIdx.x, (uint32_t)M / kTM, (uint32_t)N / kTN, tm, tn);
+  const size_t m0 = (size_t)tm * kTM, n0 = (size_t)tn * kTN;
   const char* abase = reinterpret_cast<const char*>(A + m0 * (size_t)K);
   const char* bbase = reinterpret_cast<const char*>(B + n0);
   char* cbase = reinterpret_cast<char*>(C + m0 * (size_t)N + n0);
@@ -396,7 +419,8 @@ hipError_t launch_f32(const GemmArgs& a) {
                     ((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 &&
                     ((uintptr_t)C & 15) == 0 && asm_offsets_fit(a.m, a.n, a.k);
   if (full)
-    hipLaunchKernelGGL(f32_valu_asm_kernel, grid, dim3(256), 0, a.stream, A, B, C, (int)a.n, (int)a.k);
+    hipLaunchKernelGGL(f32_valu_asm_kernel, dim3(grid.x * grid.y), dim3(256), 0, a.stream, A, B, C, (int)a.m,
+                       (int)a.n, (int)a.k);
   else
     hipLaunchKernelGGL(f32_valu_kernel<true>, grid, dim3(256), 0, a.stream, A, B, C, (int64_t)a.m,
                        (int64_t)a.n, (int64_t)a.k);
