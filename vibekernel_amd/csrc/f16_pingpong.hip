@@ -606,11 +606,12 @@ struct Epi16<half_t> {
   static __device__ __forceinline__ void flush(uint32_t wbase, half_t* Cw, int N, int lane, int half) {
     if (half == 0) return;
     const int rsub = lane >> 3, ch = lane & 7;
+    const __amdgpu_buffer_rsrc_t cr = out_rsrc(Cw);  // 128 rows: offsets below 256 N <= 2^32
 #pragma unroll
     for (int q = 0; q < 16; q++) {
       const int row = 8 * q + rsub;
       const uint4v v = epi16_read_pair(wbase, row, ch);
-      *reinterpret_cast<uint4v*>(Cw + (size_t)row * N + ch * 8) = v;
+      store_out16(cr, (uint32_t)(row * N + ch * 8) * 2u, v);
     }
   }
   // The same for a block at (row0, col0) of C that may reach past M rows or
@@ -620,11 +621,12 @@ struct Epi16<half_t> {
     if (half == 0) return;
     const int rsub = lane >> 3, ch = lane & 7;
     const bool col_in = col0 + ch * 8 < N;
+    const __amdgpu_buffer_rsrc_t cr = out_rsrc(C + (size_t)row0 * N + col0);
 #pragma unroll
     for (int q = 0; q < 16; q++) {
       const int row = 8 * q + rsub;
       const uint4v v = epi16_read_pair(wbase, row, ch);
-      if (col_in && row0 + row < M) *reinterpret_cast<uint4v*>(C + (size_t)(row0 + row) * N + col0 + ch * 8) = v;
+      if (col_in && row0 + row < M) store_out16(cr, (uint32_t)(row * N + ch * 8) * 2u, v);
     }
   }
 };
@@ -640,11 +642,12 @@ struct Epi16<float> {
   }
   static __device__ __forceinline__ void flush(uint32_t wbase, float* Cw, int N, int lane, int half) {
     const int rsub = lane >> 4, ch = lane & 15;
+    const __amdgpu_buffer_rsrc_t cr = out_rsrc(Cw + (size_t)(half * 64) * N);  // 64 rows: below 256 N
 #pragma unroll
     for (int q = 0; q < 16; q++) {
       const int row = 4 * q + rsub;
       const uint4v v = lds_read16(wbase + row * 256 + 16 * (ch ^ (row & 15)));
-      *reinterpret_cast<uint4v*>(Cw + (size_t)(half * 64 + row) * N + ch * 4) = v;
+      store_out16(cr, (uint32_t)(row * N + ch * 4) * 4u, v);
     }
     if (half == 0) wait_lgkmcnt0();  // the region is rewritten by the second half
   }
@@ -652,12 +655,13 @@ struct Epi16<float> {
                                                     int lane, int half) {
     const int rsub = lane >> 4, ch = lane & 15;
     const bool col_in = col0 + ch * 4 < N;
+    const __amdgpu_buffer_rsrc_t cr = out_rsrc(C + (size_t)(row0 + half * 64) * N + col0);
 #pragma unroll
     for (int q = 0; q < 16; q++) {
       const int row = 4 * q + rsub;
       const uint4v v = lds_read16(wbase + row * 256 + 16 * (ch ^ (row & 15)));
       const int r = row0 + half * 64 + row;
-      if (col_in && r < M) *reinterpret_cast<uint4v*>(C + (size_t)r * N + col0 + ch * 4) = v;
+      if (col_in && r < M) store_out16(cr, (uint32_t)(row * N + ch * 4) * 4u, v);
     }
     if (half == 0) wait_lgkmcnt0();
   }
