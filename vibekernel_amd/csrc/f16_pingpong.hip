@@ -621,12 +621,14 @@ struct Epi16<half_t> {
     if (half == 0) return;
     const int rsub = lane >> 3, ch = lane & 7;
     const bool col_in = col0 + ch * 8 < N;
-    const __amdgpu_buffer_rsrc_t cr = out_rsrc(C + (size_t)row0 * N + col0);
+    // Plain stores on the edge paths (version 10, the split tails with
+    // edges): the sc1 stores that help the whole tiles made the 128 x 128
+    // kernel's edge path slower at 1000^3.
 #pragma unroll
     for (int q = 0; q < 16; q++) {
       const int row = 8 * q + rsub;
       const uint4v v = epi16_read_pair(wbase, row, ch);
-      if (col_in && row0 + row < M) store_out16(cr, (uint32_t)(row * N + ch * 8) * 2u, v);
+      if (col_in && row0 + row < M) *reinterpret_cast<uint4v*>(C + (size_t)(row0 + row) * N + col0 + ch * 8) = v;
     }
   }
 };
@@ -655,13 +657,12 @@ struct Epi16<float> {
                                                     int lane, int half) {
     const int rsub = lane >> 4, ch = lane & 15;
     const bool col_in = col0 + ch * 4 < N;
-    const __amdgpu_buffer_rsrc_t cr = out_rsrc(C + (size_t)(row0 + half * 64) * N + col0);
 #pragma unroll
     for (int q = 0; q < 16; q++) {
       const int row = 4 * q + rsub;
       const uint4v v = lds_read16(wbase + row * 256 + 16 * (ch ^ (row & 15)));
       const int r = row0 + half * 64 + row;
-      if (col_in && r < M) store_out16(cr, (uint32_t)(row * N + ch * 4) * 4u, v);
+      if (col_in && r < M) *reinterpret_cast<uint4v*>(C + (size_t)r * N + col0 + ch * 4) = v;
     }
     if (half == 0) wait_lgkmcnt0();
   }

@@ -236,7 +236,10 @@ bool asm_offsets_fit(size_t m, size_t n, size_t k) {
 // 1296.5 us against 1310.4 us for the same k-loop staged through registers
 // with A transposed by 4-byte LDS stores (106.0 against 104.9 TFLOP/s).
 // Each output is one v_fmac_f32 per k in ascending order from 0: the same
-// sums, bit for bit, as the C++ kernel and the oracle.
+// sums, bit for bit, as the C++ kernel and the oracle.  C is stored with sc1
+// (written through the XCD's L2, not left dirty for the end-of-kernel
+// write-back): 1302.5 against 1314.6 us per launch at 4096^3 (3 interleaved
+// rounds on one box).
 __global__ __launch_bounds__(256) void f32_valu_asm_kernel(const float* __restrict__ A,
                                                            const float* __restrict__ B, float* __restrict__ C,
                                                            int M, int N, int K) {
@@ -382,9 +385,9 @@ __global__ __launch_bounds__(256) void f32_valu_asm_kernel(const float* __restri
       "  .irp i, 0,1,2,3\n"
       "  .irp g, 0,1,2,3\n"
       "  .if \\half == 0\n"
-      "  global_store_dwordx4 %[c_lo], v[48+16*\\i+4*\\g:51+16*\\i+4*\\g], %[cbase] offset:(\\g*256)\n"
+      "  global_store_dwordx4 %[c_lo], v[48+16*\\i+4*\\g:51+16*\\i+4*\\g], %[cbase] offset:(\\g*256) sc1\n"
       "  .else\n"
-      "  global_store_dwordx4 %[c_hi], v[48+16*\\i+4*\\g:51+16*\\i+4*\\g], %[cbase] offset:(\\g*256)\n"
+      "  global_store_dwordx4 %[c_hi], v[48+16*\\i+4*\\g:51+16*\\i+4*\\g], %[cbase] offset:(\\g*256) sc1\n"
       "  .endif\n"
       "  .endr\n"
       "  .if \\half == 0\n"

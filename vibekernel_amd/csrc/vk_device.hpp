@@ -155,9 +155,13 @@ __device__ __forceinline__ float4v load_partial(__amdgpu_buffer_rsrc_t r, uint32
 // buffer resource at the wave's block (offsets below 2^32), with sc1 (agent
 // scope), so the lines are written through the XCD's L2 as they are stored
 // instead of staying dirty there until the end-of-kernel write-back.
-// Measured on MI355X at 4096^3 (version 7, fp16 out, 3 interleaved rounds on
-// one box): 94.9 us per launch against 96.3 with plain global stores (the
-// same buffer store with the default policy: 96.3; nt: 95.2; sc0 sc1: 95.0).
+// Measured on MI355X (3 interleaved rounds per box, us per launch): version
+// 7 at 4096^3 92.36 against 93.38 with plain global stores (another box:
+// 94.9 against 96.3; the same buffer store with the default policy 96.3, nt
+// 95.2, sc0 sc1 95.0); no change at 4096 x 11008 x 4096, 4096 x 4096 x
+// 11008, 8192^3 or with fp32 output; version 11 -0.5 to -1.3 % on its whole
+// tiles (2048 x 2048 x 4096, 1024 / 512 x 4096 x 4096, 256 x 8192 x 8192).
+// The edge paths keep plain stores: at 1000^3 the sc1 form was 4 % slower.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t out_rsrc(void* base) {
   return __builtin_amdgcn_make_buffer_rsrc(base, 0, -1, kBufferWord3);
 }
