@@ -189,7 +189,7 @@ def load_bench_lib():
 class ClockSample(ctypes.Structure):
     """vkb_clock_sample (include/vk_bench.h)."""
     _fields_ = [("t_ms", ctypes.c_double), ("gfx_mhz", ctypes.c_double), ("uclk_mhz", ctypes.c_double),
-                ("socket_w", ctypes.c_double), ("gfx_activity", ctypes.c_double)]
+                ("socket_w", ctypes.c_double), ("gfx_activity", ctypes.c_double), ("xcd_mhz", ctypes.c_double * 8)]
 
 
 class ClockStats(ctypes.Structure):
@@ -291,6 +291,7 @@ def measure(clock, chunk, timed, settle_ms, per_launch_ms_hint=0.1):
         clock.stop()
     rec["timed_window_ms"] = round(t_end - t_start, 3) if t_start is not None else None
     rec["samples"] = [{"age_ms": round(s.t_ms - t_start, 2), "sclk_mhz": round(s.gfx_mhz, 1),
+                       "xcd_mhz": [round(x) for x in s.xcd_mhz],
                        "socket_w": round(s.socket_w, 1), "gfx_busy_pct": round(s.gfx_activity, 1)}
                       for s in samples]
     rec["settle"] = _aggregate([s for s in samples if s.t_ms < t_start])

@@ -69,6 +69,7 @@ typedef struct vkb_clock_sample {
   double uclk_mhz;      /* memory clock (0: not reported) */
   double socket_w;      /* socket power in W (0: not reported) */
   double gfx_activity;  /* GFX busy percentage (-1: not reported) */
+  double xcd_mhz[8];    /* SCLK of each XCD (current_gfxclks[0..7]; 0: not reported) */
 } vkb_clock_sample;
 
 /* Open the sampler for the current HIP device (VK_OK, or VK_ERR_HIP with the

@@ -170,6 +170,10 @@ struct Sampler {
         rec.socket_w = (m.current_socket_power != 0 && m.current_socket_power != 0xffff) ? m.current_socket_power
                                                                                           : 0.0;
         rec.gfx_activity = m.average_gfx_activity != 0xffff ? m.average_gfx_activity : -1.0;
+        for (int x = 0; x < 8 && x < AMDSMI_MAX_NUM_GFX_CLKS; x++) {
+            const uint16_t c = m.current_gfxclks[x];
+            rec.xcd_mhz[x] = (c != 0 && c != 0xffff) ? c : 0.0;
+        }
         {
             std::lock_guard<std::mutex> lk(dmu);
             log.push_back(rec);
