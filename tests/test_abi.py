@@ -228,3 +228,16 @@ def test_leave_one_out_instances_registered():
         assert v not in vk.versions("f16")
         assert v in vk.versions("f16", leave_one_out=True)
     assert vk.pick_version(4096, 4096, 4096) == 7
+
+
+def test_timeline_build_is_separate():
+    """The measurement build (libvk_gemm_timeline.so) exports the timestamp
+    reader; the product library does not carry it."""
+    import subprocess
+    lib = os.path.join(ROOT, "vibekernel_amd", "lib")
+    prod = subprocess.run(["nm", "-D", os.path.join(lib, "libvk_gemm.so")], capture_output=True, text=True).stdout
+    tl = subprocess.run(["nm", "-D", os.path.join(lib, "libvk_gemm_timeline.so")], capture_output=True,
+                        text=True).stdout
+    assert " T vk_gemm" in prod and " T vk_gemm" in tl
+    assert "vk_timeline_read" not in prod
+    assert " T vk_timeline_read" in tl

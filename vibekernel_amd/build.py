@@ -1,6 +1,8 @@
 """In-tree build of every native artefact (no JIT cache, no pip install).
 
 * libvk_gemm.so  -- vibekernel_amd/csrc/Makefile (hipcc --offload-arch=gfx950)
+* libvk_gemm_timeline.so -- the same with version 7's per-workgroup timestamps
+  (measurement only: vibekernel_amd/harness/timeline.py)
 * task1 harness   -- vibekernel_amd/harness/Makefile (binaries per version)
 """
 from __future__ import annotations
@@ -27,6 +29,8 @@ def build_library(force: bool = True) -> str:
     lib = os.path.join(HERE, "lib", "libvk_gemm.so")
     if not os.path.exists(lib):
         raise RuntimeError("libvk_gemm.so was not produced")
+    # the measurement build with per-workgroup timestamps (timeline.py)
+    _make(CSRC, force=force, target="timeline")
     return lib
 
 

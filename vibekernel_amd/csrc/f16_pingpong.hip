@@ -42,6 +42,25 @@
 #include <atomic>
 #include <type_traits>
 
+// Timeline build (make timeline -> libvk_gemm_timeline.so, VK_TIMELINE=1):
+// version 7's kernel also records, for waves 0 and 4 of each workgroup (one
+// per group), its XCD and the 100 MHz real-time clock at entry, after the
+// prologue (the first MFMA), after the k-loop, after the epilogue's stores
+// are issued and after they complete; vk_timeline_read() copies them out.
+// The product library is built with VK_TIMELINE=0 and records nothing.
+#ifndef VK_TIMELINE
+#define VK_TIMELINE 0
+#endif
+#if VK_TIMELINE
+constexpr int kTimelineGroups = 4096;  // workgroups recorded (the first 4096 of a launch)
+__device__ unsigned long long vk_timeline[kTimelineGroups * 2 * 8];
+extern "C" int vk_timeline_read(unsigned long long* host, int records) {
+  if (records < 0 || records > kTimelineGroups * 2) return -3;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(vk_timeline), sizeof(unsigned long long) * 8 * records, 0,
+                             hipMemcpyDeviceToHost) == hipSuccess ? 0 : -7;
+}
+#endif
+
 namespace vk {
 namespace {
 
@@ -704,7 +723,8 @@ __device__ __forceinline__ void epilogue16_edge(float4v (&acc)[8][4], uint32_t w
 template <bool kEdge = false, int kAbl = 0>
 __device__ __forceinline__ void pp16_mainloop(const half_t* __restrict__ A, const half_t* __restrict__ B, int N,
                                               int K, int m0, int n0, int kb, int nk, uint32_t lds_base, int grp,
-                                              int gw, int lane, float4v (&acc)[8][4], int M = 0) {
+                                              int gw, int lane, float4v (&acc)[8][4], int M = 0,
+                                              unsigned long long* t_first = nullptr) {
   static_assert(!(kEdge && kAbl), "the leave-one-out instances take whole tiles only");
   constexpr bool kSwzA = !(kAbl & kAblNoSwzA), kSwzB = !(kAbl & kAblNoSwzB);
   constexpr bool kDma = !(kAbl & kAblRegStage), kPP = !(kAbl & kAblNoPingPong);
@@ -971,6 +991,7 @@ __device__ __forceinline__ void pp16_mainloop(const half_t* __restrict__ A, cons
     wait_vmcnt<8>();
     lds_barrier();
   }
+  if constexpr (VK_TIMELINE != 0) *t_first = __builtin_amdgcn_s_memrealtime();
 
   for (int t = 0; t < nk; t++) {
     const int aslot = t & 1;
@@ -1022,9 +1043,27 @@ __global__ __launch_bounds__(kThreads) void f16_pp16_kernel(const half_t* __rest
   const uint32_t lds_base = lds_addr32(lds);
 
   float4v acc[8][4];
+#if VK_TIMELINE
+  const unsigned long long t0 = __builtin_amdgcn_s_memrealtime();
+  unsigned long long t1 = 0;
+  pp16_mainloop(A, B, N, K, m0, n0, 0, K / kBK, lds_base, grp, gw, lane, acc, 0, &t1);
+  const unsigned long long t2 = __builtin_amdgcn_s_memrealtime();
+  epilogue16<OutT>(acc, lds_base + wave * (128 * 64 * 2), C + (size_t)(m0 + grp * 128) * N + n0 + gw * 64, N,
+                   lane_from_exec());
+  const unsigned long long t3 = __builtin_amdgcn_s_memrealtime();
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  const unsigned long long t4 = __builtin_amdgcn_s_memrealtime();
+  unsigned xcc;
+  asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+  if (lane_from_exec() == 0 && gw == 0 && blockIdx.x < kTimelineGroups) {
+    unsigned long long* r = vk_timeline + (blockIdx.x * 2 + grp) * 8;
+    r[0] = t0; r[1] = t1; r[2] = t2; r[3] = t3; r[4] = t4; r[5] = xcc & 15u; r[6] = tm; r[7] = tn;
+  }
+#else
   pp16_mainloop(A, B, N, K, m0, n0, 0, K / kBK, lds_base, grp, gw, lane, acc);
   epilogue16<OutT>(acc, lds_base + wave * (128 * 64 * 2), C + (size_t)(m0 + grp * 128) * N + n0 + gw * 64, N,
                    lane_from_exec());
+#endif
 }
 
 template <typename OutT>
