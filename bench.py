@@ -39,8 +39,8 @@ the spec peak at 2.4 GHz.
 
 Library ceiling (after the timed region, the output check and the reference
 loop; `--no-library-ceiling` skips it; never part of any product path): the
-same product on the same A and B through torch.matmul (fp16 out, fp32
-accumulation) under the same protocol -- a settle phase of the same length
+same product on the same A and B through torch.matmul (fp32 accumulation;
+for fp32 inputs with TF32 off) under the same protocol -- a settle phase of the same length
 ending on a metrics refresh, `--warmup` launches, a device synchronisation,
 `--steps` launches back to back between one event pair -- once per BLAS
 backend torch offers on ROCm (hipBLASLt, rocBLAS, Composable Kernel), reported as
@@ -311,7 +311,9 @@ def library_ceiling(A, B, out, args, cus, flop_clk_cu, peak, clock):
     bk = torch.backends.cuda
     saved_backend = bk.preferred_blas_library()
     saved_red = bk.matmul.allow_fp16_reduced_precision_reduction
+    saved_tf32 = bk.matmul.allow_tf32
     bk.matmul.allow_fp16_reduced_precision_reduction = False  # fp32 accumulation throughout
+    bk.matmul.allow_tf32 = False  # fp32 inputs multiplied in fp32
     res = {}
     tuned = False
     try:
@@ -322,9 +324,9 @@ def library_ceiling(A, B, out, args, cus, flop_clk_cu, peak, clock):
             tuned = True
 
         def mm():
-            if out == "f16":
+            if A.dtype == C2.dtype:
                 torch.matmul(A, B, out=C2)
-            else:
+            else:  # fp16 in, fp32 out
                 torch.mm(A, B, out_dtype=torch.float32, out=C2)
 
         # torch's names on ROCm: "hipblaslt" (hipBLASLt), "hipblas" (rocBLAS
@@ -385,6 +387,7 @@ def library_ceiling(A, B, out, args, cus, flop_clk_cu, peak, clock):
     finally:
         bk.preferred_blas_library(saved_backend)
         bk.matmul.allow_fp16_reduced_precision_reduction = saved_red
+        bk.matmul.allow_tf32 = saved_tf32
         if tuned:
             torch.cuda.tunable.tuning_enable(False)
             torch.cuda.tunable.enable(False)
@@ -723,7 +726,7 @@ def main():
         "reference_best_a100_frac_of_peak": 0.897,
         "roofline": roofline,
     }
-    if not args.no_library_ceiling and dtype == "f16":
+    if not args.no_library_ceiling:
         lib_ceiling = library_ceiling(A, B, out, args, cus, flop_clk_cu, peak, clock)
         if lib_ceiling["tflops"]:
             lib_ceiling["product_over_library"] = round(tflops / lib_ceiling["tflops"], 4)
