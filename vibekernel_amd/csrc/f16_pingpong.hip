@@ -597,7 +597,7 @@ constexpr int kAblRegStage = 4;    // global -> VGPR -> ds_write_b128 instead of
 constexpr int kAblB2 = 8;          // B ring of 2 slots: B(t+1) loaded during compute(t) (prefetch 1 ahead)
 constexpr int kAblNoPingPong = 16; // both groups in phase: all 8 waves read, then all compute
 constexpr int kAblNoXcd = 32;      // grouped raster without the XCD remap
-constexpr int kAblNoChain = 64;    // MFMAs rotate over the 32 accumulators (k-step 0 of all, then 1)
+constexpr int kAblNoChain = 64;    // MFMAs rotate over the 32 accumulators (each one's first k-step for all, then the second)
 
 template <int kAbl>
 constexpr int lds_bytes_of() {
@@ -924,8 +924,14 @@ __device__ __forceinline__ void pp16_mainloop(const half_t* __restrict__ A, cons
   // accumulator input is the first one's result): measured on MI355X with a
   // pure 16x16x32 stream at the power limit, such chains of 2 raise the
   // sustained clock by ~4% over rotating through the accumulators, at the
-  // same issue rate.  Per element the sum order (k-step 0, then 1) is
-  // unchanged.  The scheduling barriers keep the pairs adjacent.
+  // same issue rate.  The chains run along each row of blocks and back along
+  // the next (j = 3 .. 0 on odd i), and accumulator (i, j) takes k-step
+  // (i ^ j) & 1 first, so every chain starts on the operand register the one
+  // before ended on (A fragment within a row, B at a row change): fewer
+  // operand bits toggle, and at 4096^3, 8192^3 and 4096 x 4096 x 11008 the
+  // board held its power limit 10-11 MHz higher for the same cycles per
+  // launch (+0.5-0.7 %, 5 interleaved pairs on one box).  The scheduling
+  // barriers keep the pairs adjacent.
   // Load d of the k-tile described by `o`: direct-to-LDS, or (kAblRegStage)
   // into stg[d], written to LDS four loads later (the compiler waits for
   // that load alone: vmcnt(3)), the last four after the MFMAs.
@@ -943,10 +949,12 @@ __device__ __forceinline__ void pp16_mainloop(const half_t* __restrict__ A, cons
 #pragma unroll
       for (int i = 0; i < 8; i++) {
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-          acc[i][j] = mfma16x16x32(fb[0][j], fa[0][i], acc[i][j]);
+        for (int jj = 0; jj < 4; jj++) {
+          const int j = (i & 1) ? 3 - jj : jj;
+          const int k0 = (i ^ j) & 1;
+          acc[i][j] = mfma16x16x32(fb[k0][j], fa[k0][i], acc[i][j]);
           __builtin_amdgcn_sched_barrier(0);
-          acc[i][j] = mfma16x16x32(fb[1][j], fa[1][i], acc[i][j]);
+          acc[i][j] = mfma16x16x32(fb[k0 ^ 1][j], fa[k0 ^ 1][i], acc[i][j]);
           __builtin_amdgcn_sched_barrier(0);
         }
         load_step(i, o);
@@ -959,7 +967,8 @@ __device__ __forceinline__ void pp16_mainloop(const half_t* __restrict__ A, cons
         for (int i = 0; i < 8; i++) {
 #pragma unroll
           for (int j = 0; j < 4; j++) {
-            acc[i][j] = mfma16x16x32(fb[s2][j], fa[s2][i], acc[i][j]);
+            const int k = s2 ^ ((i ^ j) & 1);  // the chained form's per-element order
+            acc[i][j] = mfma16x16x32(fb[k][j], fa[k][i], acc[i][j]);
             __builtin_amdgcn_sched_barrier(0);
           }
           if (i & 1) {

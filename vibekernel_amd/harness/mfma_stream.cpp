@@ -9,6 +9,16 @@
 //   rotate   the same instructions rotating over the 16 accumulators
 //   m32      v_mfma_f32_32x32x16_f16 (4 accumulators of 16 registers), rotating
 //   zero     chain2 with all-zero operands
+//   chain4   as chain2 with each accumulator's four MFMAs back to back
+//   chain8   as chain2 with each accumulator's eight MFMAs back to back
+//   gemm     chains of 2 over a GEMM's operands (accumulator (i, j) takes
+//            A(i, k) B(j, k) for k = 0, 1; A, B registers change with k),
+//            blocks in row order, every chain k = 0 then 1 (version 7's
+//            order): consecutive MFMAs share no operand register
+//   snake    the same chains, alternate ones in k = 1, 0 order and the
+//            blocks snaked along j, so that each chain starts on the
+//            operand register (A, or B at a row change) the previous one
+//            ended on
 //
 // No GEMM reaches more than its mix's figure on the same board: the figure
 // prices the MFMA work alone, with no loads, LDS traffic or barriers.
@@ -30,7 +40,6 @@ typedef float float4v __attribute__((ext_vector_type(4)));
 typedef float float16v __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 512;       // 8 waves: 2 per SIMD
-constexpr int kMfmaPerIter = 32;
 constexpr int kLdsPin = 96 * 1024;
 
 template <int kMode>
@@ -76,14 +85,32 @@ __global__ __launch_bounds__(kThreads) void mfma_stream(const half8* __restrict_
             acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[(j + r) & 3], b[j >> 2], acc[j], 0, 0, 0);
             __builtin_amdgcn_sched_barrier(0);
           }
-      } else {  // chains of 2: each accumulator's two MFMAs back to back
+      } else if constexpr (kMode == 5 || kMode == 6) {
+        // 4 x 4 blocks; A(i, k) = a[2 (i & 1) + k], B(j, k) = b[2 (j & 1) + k]
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[j & 3], b[j >> 2], acc[j], 0, 0, 0);
-          __builtin_amdgcn_sched_barrier(0);
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[(j + 1) & 3], b[j >> 2], acc[j], 0, 0, 0);
-          __builtin_amdgcn_sched_barrier(0);
-        }
+        for (int i = 0; i < 4; i++)
+#pragma unroll
+          for (int jj = 0; jj < 4; jj++) {
+            const int j = kMode == 6 && (i & 1) ? 3 - jj : jj;
+            const int c = 4 * i + jj;                       // chain number
+            const int k0 = kMode == 6 ? (c & 1) : 0;        // first k of the chain
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+              const int k = k0 ^ r;
+              acc[4 * i + j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[2 * (i & 1) + k], b[2 * (j & 1) + k],
+                                                                      acc[4 * i + j], 0, 0, 0);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          }
+      } else {  // chains of kChain: each accumulator's MFMAs back to back
+        constexpr int kChain = kMode == 3 ? 4 : kMode == 4 ? 8 : 2;
+#pragma unroll
+        for (int j = 0; j < 16; j++)
+#pragma unroll
+          for (int c = 0; c < kChain; c++) {
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[(j + c) & 3], b[j >> 2], acc[j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+          }
       }
     }
 #pragma unroll
@@ -97,6 +124,7 @@ struct Mix {
   int mode;
   bool zero;
   double flop_per_mfma;
+  int mfma_per_iter;  // per wave
 };
 
 int main(int argc, char** argv) {
@@ -124,23 +152,39 @@ int main(int argc, char** argv) {
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsPin));
   PLAYGROUND_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_stream<2>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsPin));
+  PLAYGROUND_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_stream<3>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsPin));
+  PLAYGROUND_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_stream<4>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsPin));
+  PLAYGROUND_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_stream<5>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsPin));
+  PLAYGROUND_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_stream<6>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsPin));
 
-  const Mix mixes[] = {{"chain2", 0, false, 16.0 * 16 * 32 * 2},
-                       {"rotate", 1, false, 16.0 * 16 * 32 * 2},
-                       {"m32", 2, false, 32.0 * 32 * 16 * 2},
-                       {"zero", 0, true, 16.0 * 16 * 32 * 2}};
+  const Mix mixes[] = {{"chain2", 0, false, 16.0 * 16 * 32 * 2, 32}, {"rotate", 1, false, 16.0 * 16 * 32 * 2, 32},
+                       {"m32", 2, false, 32.0 * 32 * 16 * 2, 32},   {"zero", 0, true, 16.0 * 16 * 32 * 2, 32},
+                       {"chain4", 3, false, 16.0 * 16 * 32 * 2, 64}, {"chain8", 4, false, 16.0 * 16 * 32 * 2, 128},
+                       {"gemm", 5, false, 16.0 * 16 * 32 * 2, 32},   {"snake", 6, false, 16.0 * 16 * 32 * 2, 32}};
   for (const Mix& mx : mixes) {
     const half8* src = mx.zero ? d_zero : d_rand;
     // about 1 ms per launch at the full rate
-    const int iters = mx.mode == 2 ? 1024 : 2048;
+    const int iters = (mx.mode == 2 ? 1024 : 2048) * 32 / mx.mfma_per_iter;
     // 96 KB of (unused) dynamic LDS per workgroup: one workgroup per CU
     auto launch = [&]() {
       if (mx.mode == 0)
         hipLaunchKernelGGL(mfma_stream<0>, dim3(grid), dim3(kThreads), kLdsPin, 0, src, d_out, iters);
       else if (mx.mode == 1)
         hipLaunchKernelGGL(mfma_stream<1>, dim3(grid), dim3(kThreads), kLdsPin, 0, src, d_out, iters);
-      else
+      else if (mx.mode == 2)
         hipLaunchKernelGGL(mfma_stream<2>, dim3(grid), dim3(kThreads), kLdsPin, 0, src, d_out, iters);
+      else if (mx.mode == 3)
+        hipLaunchKernelGGL(mfma_stream<3>, dim3(grid), dim3(kThreads), kLdsPin, 0, src, d_out, iters);
+      else if (mx.mode == 4)
+        hipLaunchKernelGGL(mfma_stream<4>, dim3(grid), dim3(kThreads), kLdsPin, 0, src, d_out, iters);
+      else if (mx.mode == 5)
+        hipLaunchKernelGGL(mfma_stream<5>, dim3(grid), dim3(kThreads), kLdsPin, 0, src, d_out, iters);
+      else
+        hipLaunchKernelGGL(mfma_stream<6>, dim3(grid), dim3(kThreads), kLdsPin, 0, src, d_out, iters);
     };
     bool sampling = false;
     const auto t0 = std::chrono::steady_clock::now();
@@ -170,7 +214,7 @@ int main(int argc, char** argv) {
       vkb_clock_stats st;
       vkb_clock_stop(&st);
     }
-    const double flop = (double)grid * (kThreads / 64) * kMfmaPerIter * iters * mx.flop_per_mfma * 20;
+    const double flop = (double)grid * (kThreads / 64) * mx.mfma_per_iter * iters * mx.flop_per_mfma * 20;
     const double tflops = flop / (ms * 1e-3) / 1e12;
     std::printf("{\"mix\": \"%s\", \"tflops\": %.1f, \"ms_per_launch\": %.4f, \"cus\": %d", mx.name, tflops, ms / 20,
                 cus);
