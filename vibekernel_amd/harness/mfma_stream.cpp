@@ -19,6 +19,7 @@
 //            blocks snaked along j, so that each chain starts on the
 //            operand register (A, or B at a row change) the previous one
 //            ended on
+//   *_w1     the same mix with one wave per SIMD (256-thread workgroups)
 //
 // No GEMM reaches more than its mix's figure on the same board: the figure
 // prices the MFMA work alone, with no loads, LDS traffic or barriers.
@@ -125,6 +126,7 @@ struct Mix {
   bool zero;
   double flop_per_mfma;
   int mfma_per_iter;  // per wave
+  int threads;        // per workgroup (one per CU): 512 = 2 waves per SIMD, 256 = 1
 };
 
 int main(int argc, char** argv) {
@@ -161,10 +163,13 @@ int main(int argc, char** argv) {
   PLAYGROUND_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_stream<6>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsPin));
 
-  const Mix mixes[] = {{"chain2", 0, false, 16.0 * 16 * 32 * 2, 32}, {"rotate", 1, false, 16.0 * 16 * 32 * 2, 32},
-                       {"m32", 2, false, 32.0 * 32 * 16 * 2, 32},   {"zero", 0, true, 16.0 * 16 * 32 * 2, 32},
-                       {"chain4", 3, false, 16.0 * 16 * 32 * 2, 64}, {"chain8", 4, false, 16.0 * 16 * 32 * 2, 128},
-                       {"gemm", 5, false, 16.0 * 16 * 32 * 2, 32},   {"snake", 6, false, 16.0 * 16 * 32 * 2, 32}};
+  constexpr double k16 = 16.0 * 16 * 32 * 2;
+  const Mix mixes[] = {{"chain2", 0, false, k16, 32, 512},    {"rotate", 1, false, k16, 32, 512},
+                       {"m32", 2, false, 32.0 * 32 * 16 * 2, 32, 512},
+                       {"zero", 0, true, k16, 32, 512},      {"chain4", 3, false, k16, 64, 512},
+                       {"chain8", 4, false, k16, 128, 512},  {"gemm", 5, false, k16, 32, 512},
+                       {"snake", 6, false, k16, 32, 512},    {"chain2_w1", 0, false, k16, 32, 256},
+                       {"rotate_w1", 1, false, k16, 32, 256}, {"snake_w1", 6, false, k16, 32, 256}};
   for (const Mix& mx : mixes) {
     const half8* src = mx.zero ? d_zero : d_rand;
     // about 1 ms per launch at the full rate
@@ -172,19 +177,19 @@ int main(int argc, char** argv) {
     // 96 KB of (unused) dynamic LDS per workgroup: one workgroup per CU
     auto launch = [&]() {
       if (mx.mode == 0)
-        hipLaunchKernelGGL(mfma_stream<0>, dim3(grid), dim3(kThreads), kLdsPin, 0, src, d_out, iters);
+        hipLaunchKernelGGL(mfma_stream<0>, dim3(grid), dim3(mx.threads), kLdsPin, 0, src, d_out, iters);
       else if (mx.mode == 1)
-        hipLaunchKernelGGL(mfma_stream<1>, dim3(grid), dim3(kThreads), kLdsPin, 0, src, d_out, iters);
+        hipLaunchKernelGGL(mfma_stream<1>, dim3(grid), dim3(mx.threads), kLdsPin, 0, src, d_out, iters);
       else if (mx.mode == 2)
-        hipLaunchKernelGGL(mfma_stream<2>, dim3(grid), dim3(kThreads), kLdsPin, 0, src, d_out, iters);
+        hipLaunchKernelGGL(mfma_stream<2>, dim3(grid), dim3(mx.threads), kLdsPin, 0, src, d_out, iters);
       else if (mx.mode == 3)
-        hipLaunchKernelGGL(mfma_stream<3>, dim3(grid), dim3(kThreads), kLdsPin, 0, src, d_out, iters);
+        hipLaunchKernelGGL(mfma_stream<3>, dim3(grid), dim3(mx.threads), kLdsPin, 0, src, d_out, iters);
       else if (mx.mode == 4)
-        hipLaunchKernelGGL(mfma_stream<4>, dim3(grid), dim3(kThreads), kLdsPin, 0, src, d_out, iters);
+        hipLaunchKernelGGL(mfma_stream<4>, dim3(grid), dim3(mx.threads), kLdsPin, 0, src, d_out, iters);
       else if (mx.mode == 5)
-        hipLaunchKernelGGL(mfma_stream<5>, dim3(grid), dim3(kThreads), kLdsPin, 0, src, d_out, iters);
+        hipLaunchKernelGGL(mfma_stream<5>, dim3(grid), dim3(mx.threads), kLdsPin, 0, src, d_out, iters);
       else
-        hipLaunchKernelGGL(mfma_stream<6>, dim3(grid), dim3(kThreads), kLdsPin, 0, src, d_out, iters);
+        hipLaunchKernelGGL(mfma_stream<6>, dim3(grid), dim3(mx.threads), kLdsPin, 0, src, d_out, iters);
     };
     bool sampling = false;
     const auto t0 = std::chrono::steady_clock::now();
@@ -214,10 +219,10 @@ int main(int argc, char** argv) {
       vkb_clock_stats st;
       vkb_clock_stop(&st);
     }
-    const double flop = (double)grid * (kThreads / 64) * mx.mfma_per_iter * iters * mx.flop_per_mfma * 20;
+    const double flop = (double)grid * (mx.threads / 64) * mx.mfma_per_iter * iters * mx.flop_per_mfma * 20;
     const double tflops = flop / (ms * 1e-3) / 1e12;
-    std::printf("{\"mix\": \"%s\", \"tflops\": %.1f, \"ms_per_launch\": %.4f, \"cus\": %d", mx.name, tflops, ms / 20,
-                cus);
+    std::printf("{\"mix\": \"%s\", \"waves_per_simd\": %d, \"tflops\": %.1f, \"ms_per_launch\": %.4f, \"cus\": %d",
+                mx.name, mx.threads / 256, tflops, ms / 20, cus);
     if (ns > 0) {
       const vkb_clock_sample& s = smp[(ns < 64 ? ns : 64) - 1];  // the last refresh before the timed launches
       std::printf(", \"sclk_mhz\": %.1f, \"socket_w\": %.1f, \"xcd_mhz\": [", s.gfx_mhz, s.socket_w);
