@@ -3,7 +3,8 @@ turned off each (A swizzle, B swizzle, direct-to-LDS loads, the third B
 slot, the ping-pong, the XCD-aware tile order, the accumulator chains).
 
 None of them changes what is summed or in which order (per element: k-tiles
-ascending, k-step 0 then 1 of each, the MFMA's own sum over its 32 k), so
+ascending, k-step (i ^ j) & 1 of each first for the 16 x 16 block (i, j)
+of a wave's 128 x 64 block, the MFMA's own sum over its 32 k), so
 each must equal version 7 bit for bit on the same inputs; integer products
 must be exact; and at the headline 4096^3 the fp32 output must lie within
 the fp32 accumulation bound of the exact (fp64) product.  Small shapes cover

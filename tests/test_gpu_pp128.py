@@ -5,7 +5,8 @@ empty.
 Bars:
 * bitwise equal to version 7 wherever both accept the shape (M, N multiples
   of 256, K of 128): every output element is the same chain of 16x16x32 MFMAs
-  over 32-deep k-steps in ascending order, so any difference is a wrong
+  over 32-deep k-steps in the same order (64-deep k-tiles ascending; in
+  each, k-step ((row / 16) ^ (column / 16)) & 1 first), so any difference is a wrong
   fragment, swizzle, ring slot or store;
 * fp32 and fp16 output against the exact product within the fp32
   accumulation bound (fp16: plus half an fp16 ulp), every element written

@@ -3,7 +3,8 @@ and 64 x 32 wave blocks without the ping-pong -- every wave computes its
 64-deep k-tile while reading the next one's fragments.
 
 Each element is the same chain of 16x16x32 MFMAs over 32-deep k-steps in
-ascending order as in version 11, with the same zero padding at the edges
+the same order as in version 11 (64-deep halves ascending, k-step
+(i ^ j) & 1 of each first), with the same zero padding at the edges
 and the same k-slices where K is split, so the bar is bitwise equality with
 version 11 on every shape, whole, edge and split, fp16 and fp32 output (any
 wrong fragment, slot, swizzle, wait or piece shows up as a different bit);

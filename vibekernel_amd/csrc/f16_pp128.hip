@@ -416,15 +416,20 @@ __global__ __launch_bounds__(kThreads) void f16_pp128_kernel(const half_t* __res
       }
     });
   };
-  // 32 MFMAs, each accumulator's 4 k-steps back to back (k ascending), and
-  // the 8 loads described by `o`, one after each accumulator.
+  // 32 MFMAs, each accumulator's 4 k-steps back to back, and the 8 loads
+  // described by `o`, one after each accumulator.  Version 7's per-element
+  // order: in each 64-deep half of the k-tile, block (i, j) takes k-step
+  // (i ^ j) & 1 of the half first (the wave's block offsets are multiples of
+  // 32, so i and j have the parity of the global 16-row and 16-column block
+  // indices, as in version 7's 128 x 64 wave blocks).
   auto compute_and_load = [&](const DmaOps& o) {
 #pragma unroll
     for (int i = 0; i < 4; i++) {
 #pragma unroll
       for (int j = 0; j < 2; j++) {
 #pragma unroll
-        for (int s = 0; s < 4; s++) {
+        for (int s4 = 0; s4 < 4; s4++) {
+          const int s = s4 ^ ((i ^ j) & 1);
           acc[i][j] = mfma16x16x32(fb[s][j], fa[s][i], acc[i][j]);
           __builtin_amdgcn_sched_barrier(0);
         }
@@ -919,9 +924,9 @@ hipError_t launch(const GemmArgs& a) {
 //    may still fly) and barrier;
 //  * loads per step: wave w loads A rows 16 w .. 16 w + 15 (2 loads of 8
 //    rows) and B k-rows 8 w .. 8 w + 7 (2 loads of 4 k-rows);
-//  * each element is the same chain of MFMAs over 32-deep k-steps in
-//    ascending order as in versions 7 and 11 (bitwise equal where they run
-//    whole tiles).  Epilogue, edges and split hand-off are version 11's.
+//  * each element is the same chain of MFMAs over 32-deep k-steps as in
+//    versions 7 and 11 (64-deep k-tiles ascending, k-step (i ^ j) & 1 of each
+//    first; bitwise equal where they run whole tiles).  Epilogue, edges and split hand-off are version 11's.
 namespace pp128n {
 
 using pp128w::kARow;
@@ -1082,18 +1087,20 @@ __global__ __launch_bounds__(kThreads) void f16_pp128n_kernel(const half_t* __re
     static_for<16>([&](auto rc) { read_one(f, sl, rc); });
   };
   // One step: the 16 MFMAs of `cur` (each accumulator's 2 k-steps back to
-  // back), after each one a read of `nxt` (when there is a next k-tile), and
-  // the 4 loads of `o` after every 4 MFMAs.
+  // back, k-step (i ^ j) & 1 first as in versions 7 and 11), after each one
+  // a read of `nxt` (when there is a next k-tile), and the 4 loads of `o`
+  // after every 4 MFMAs.
   auto step = [&](const Frags& cur, Frags& nxt, int nslot, bool has_next, const Ops& o) {
     const uint32_t sl = lds_base + (uint32_t)(nslot * kSlot);
     static_for<8>([&](auto xc) {
       constexpr int x = decltype(xc)::value;
       constexpr int i = x >> 1, j = x & 1;
-      acc[i][j] = mfma16x16x32(cur.b[0][j], cur.a[0][i], acc[i][j]);
+      constexpr int k0 = (i ^ j) & 1;
+      acc[i][j] = mfma16x16x32(cur.b[k0][j], cur.a[k0][i], acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
       if (has_next) read_one(nxt, sl, std::integral_constant<int, 2 * x>{});
       __builtin_amdgcn_sched_barrier(0);
-      acc[i][j] = mfma16x16x32(cur.b[1][j], cur.a[1][i], acc[i][j]);
+      acc[i][j] = mfma16x16x32(cur.b[k0 ^ 1][j], cur.a[k0 ^ 1][i], acc[i][j]);
       __builtin_amdgcn_sched_barrier(0);
       if (has_next) read_one(nxt, sl, std::integral_constant<int, 2 * x + 1>{});
       __builtin_amdgcn_sched_barrier(0);
