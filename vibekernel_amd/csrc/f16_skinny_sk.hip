@@ -49,6 +49,25 @@
 #include <atomic>
 #include <type_traits>
 
+// Timeline build (make timeline -> libvk_gemm_timeline.so, VK_TIMELINE=1):
+// wave 0 of each workgroup also records its XCD, its k part and step count,
+// and the 100 MHz real-time clock at entry, at the end of its k-loop and when
+// it leaves (after its partial's hand-off, or after the sums for the last
+// arrival); vk_timeline_sk_read() copies them out.  The product library is
+// built with VK_TIMELINE=0 and records nothing.
+#ifndef VK_TIMELINE
+#define VK_TIMELINE 0
+#endif
+#if VK_TIMELINE
+constexpr int kSkTimelineGroups = 4096;  // workgroups recorded (the first 4096 of a launch)
+__device__ unsigned long long vk_timeline_sk[kSkTimelineGroups * 6];
+extern "C" int vk_timeline_sk_read(unsigned long long* host, int records) {
+  if (records < 0 || records > kSkTimelineGroups) return -3;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(vk_timeline_sk), sizeof(unsigned long long) * 6 * records, 0,
+                             hipMemcpyDeviceToHost) == hipSuccess ? 0 : -7;
+}
+#endif
+
 namespace vk {
 namespace {
 
@@ -148,12 +167,29 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
 
   const int cid = blockIdx.x;
   const int cb = cid / ks_count, kp = cid - cb * ks_count;
+#if VK_TIMELINE
+  const unsigned long long tl0 = __builtin_amdgcn_s_memrealtime();
+  unsigned long long tl1 = 0;
+#endif
   const int n0 = cb * NC;
   // Piece kp of the K / 32 steps: steps floor(kp T / ks) .. floor((kp + 1) T / ks) - 1.
   const int tsteps = K / kKStep;
   const int sbeg = (int)((long long)kp * tsteps / ks_count);
   const int kbeg = sbeg * kKStep;
   const int nsteps = (int)((long long)(kp + 1) * tsteps / ks_count) - sbeg;
+#if VK_TIMELINE
+  auto tl_record = [&]() {
+    if (threadIdx.x == 0 && cid < kSkTimelineGroups) {
+      unsigned xcc;
+      asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+      unsigned long long* r = vk_timeline_sk + cid * 6;
+      r[0] = tl0; r[1] = tl1; r[2] = __builtin_amdgcn_s_memrealtime(); r[3] = xcc & 15u;
+      r[4] = (unsigned long long)nsteps; r[5] = (unsigned long long)kp;
+    }
+  };
+#else
+  auto tl_record = []() {};
+#endif
 
   // Direct-to-LDS duty per k-step.  B: load i covers k-rows 8w + i*R .. +R-1
   // (R = 1024 / (2 NC) rows of NC/8 chunks; lane l: row l / (NC/8), slot
@@ -289,6 +325,9 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
   else
     pipeline(std::integral_constant<int, kNaLo>{});
   wait_vmcnt<0>();  // clamped tail refills
+#if VK_TIMELINE
+  tl1 = __builtin_amdgcn_s_memrealtime();
+#endif
 
   // Epilogue.  D layout: lane l, register e of block (r, c) -> row
   // 16 r + 4 (l / 16) + e, column kWaveCols * w + 16 c + l % 16 of the block.
@@ -308,6 +347,7 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
   if (ks_count == 1) {
 #pragma unroll
     for (int b = 0; b < NB; b++) store_c(b, acc[b / G::kColBlocks][b % G::kColBlocks]);
+    tl_record();
     return;
   }
 
@@ -335,7 +375,10 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
     wait_vmcnt0_ordered();  // the partial is in memory before the counter moves
     unsigned old = 0;
     if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (__builtin_amdgcn_readfirstlane(old) != (unsigned)(ks_count - 1)) return;
+    if (__builtin_amdgcn_readfirstlane(old) != (unsigned)(ks_count - 1)) {
+      tl_record();
+      return;
+    }
   }
   // The counter read that made this wave the last stays before the reads of
   // the other parts.
@@ -379,6 +422,7 @@ __global__ __launch_bounds__(kThreads, 1) void f16_skinny_sk_kernel(const half_t
     default: fold(std::integral_constant<int, 8>{}); break;
   }
   if (lane == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  tl_record();
 }
 
 constexpr int kMaxRows = 256;

@@ -3,10 +3,12 @@
 // Same operator as fp32 version 1 (f32_valu.hip: the harness's fp32 path,
 // results/naive_cycle4/include/playground/system.hpp:35-41, ground truth
 // matmul_f32_v0_cblas.cpp:8-12), computed with v_mfma_f32_32x32x2_f32.
-// Measured on MI355X with random, changing operands on all CUs (2 waves per
-// SIMD): that instruction sustains 148.7 TFLOP/s of the 157.3 dense fp32
-// figure, while the 16x16x4 form reaches only ~74 and the VALU kernel (plain
-// FMAs, LDS-bound at 8x8 outputs per thread) 89.6 at 4096^3.  An fp32 MFMA
+// Measured on MI355X with random operands on all CUs (2 waves per SIMD,
+// harness/mfma_stream): that instruction over 8 accumulators in rotation
+// sustains 153.3 TFLOP/s (0.983 of the 157.3 dense fp32 figure at the
+// measured 2.38 GHz; fp32 MFMAs stay below the board's power limit) and the
+// 16x16x4 form 152.7; a 16x16x4 version of this kernel measured slower.  An
+// fp32 MFMA
 // does 64 FLOP per clock per SIMD -- 16x fewer than the fp16 form -- so the
 // operand traffic per cycle is small and the kernel can be simple:
 //  * 256x256 tile, 8 waves; wave w owns rows 128*(w/4) .. +127 and columns
@@ -15,7 +17,8 @@
 //    direct-to-LDS loads, one barrier per k-tile: BK = 32 in 2 stages of 64 KB
 //    when K allows, else BK = 16 in 4 stages of 32 KB;
 //  * per k-tile each wave reads its fragments (BK/2 ds_read_b128 of A, BK
-//    ds_read_b32 of B) and issues 4*BK MFMAs of 64 cycles.
+//    ds_read_b32 of B) and issues 4*BK MFMAs of 64 cycles, with its loads of
+//    a later k-tile going out one after each of the first MFMA steps.
 // Fragments: the MFMA takes lane l's A value as X[l%32][l/32] and its B value
 // as Y[l/32][l%32] (2 k per instruction).  Step s of a k-tile pairs k = s
 // (lanes 0..31) with k = BK/2 + s (lanes 32..63), so a lane's A values for
@@ -155,6 +158,33 @@ __global__ __launch_bounds__(kThreads) void f32_mfma_kernel(const float* __restr
         dma16(gB + (size_t)kt * BK * N * 4, voffB[d], s + G::kABytes + (G::kDmaB * wave + d) * 1024);
     }
   };
+  // Load d of the k-tile (A loads first, then B), one at a time: inside the
+  // k-loop the loads of a later k-tile go out one after each MFMA step
+  // instead of in a burst after the barrier (measured +1.1 % at 4096^3,
+  // +1.6 % on version 3 at 4000^3: a wave stalled behind its burst of loads
+  // issues no MFMA).
+  auto issue_one = [&](int kt, int slot, int d) {
+    const uint32_t s = lds_base + slot * G::kStageBytes;
+    if constexpr (kEdge) {
+      const uint32_t kleft = (uint32_t)(K - kt * BK);
+      const uint32_t soffA = (uint32_t)(m0 * K + kt * BK) * 4u;
+      const uint32_t soffB = (uint32_t)(kt * BK * N + n0) * 4u;
+      if (d < G::kDmaA) {
+        const uint32_t off = ((akin >> (5 * d)) & 31u) < kleft ? voffA[d] : sizeA;
+        dma16_buf(rsrcA, off, soffA, s + (G::kDmaA * wave + d) * 1024);
+      } else {
+        const int e = d - G::kDmaA;
+        dma16_buf(rsrcB, voffB[e], soffB, s + G::kABytes + (G::kDmaB * wave + e) * 1024);
+      }
+    } else {
+      if (d < G::kDmaA) {
+        dma16(gA + (size_t)kt * BK * 4, voffA[d], s + (G::kDmaA * wave + d) * 1024);
+      } else {
+        const int e = d - G::kDmaA;
+        dma16(gB + (size_t)kt * BK * N * 4, voffB[e], s + G::kABytes + (G::kDmaB * wave + e) * 1024);
+      }
+    }
+  };
 
   // ---- fragment addresses inside a stage: lane half h takes k = (BK/2) h
   // + s at step s ----
@@ -194,7 +224,7 @@ __global__ __launch_bounds__(kThreads) void f32_mfma_kernel(const float* __restr
     // also ends every wave's reads of the slot the next issue refills.
     wait_vmcnt<(G::kNS - 2) * G::kDma>();
     lds_barrier();
-    issue(min(t + G::kNS - 1, nk - 1), (t + G::kNS - 1) % G::kNS);
+    const int kt_next = min(t + G::kNS - 1, nk - 1), slot_next = (t + G::kNS - 1) % G::kNS;
     const uint32_t s = lds_base + (t % G::kNS) * G::kStageBytes;
     float a[4][G::kSteps], b[2][G::kSteps];
 #pragma unroll
@@ -209,13 +239,20 @@ __global__ __launch_bounds__(kThreads) void f32_mfma_kernel(const float* __restr
     for (int bj = 0; bj < 2; bj++)
 #pragma unroll
       for (int st = 0; st < G::kSteps; st++) b[bj][st] = lds_read_f32(s + boff[bj] + st * 1024);
+    static_assert(G::kDma <= G::kSteps, "one load per MFMA step");
 #pragma unroll
-    for (int st = 0; st < G::kSteps; st++)
+    for (int st = 0; st < G::kSteps; st++) {
 #pragma unroll
       for (int bi = 0; bi < 4; bi++)
 #pragma unroll
         for (int bj = 0; bj < 2; bj++)
           acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(a[bi][st], b[bj][st], acc[bi][bj], 0, 0, 0);
+      if (st < G::kDma) {
+        __builtin_amdgcn_sched_barrier(0);
+        issue_one(kt_next, slot_next, st);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    }
   }
   wait_vmcnt<0>();  // clamped refills past the last k-tile
 

@@ -1,5 +1,6 @@
 // mfma_stream.cpp -- the matrix cores' own ceiling under MI355X's power
-// limit: every CU runs nothing but fp16 MFMAs on operands held in registers
+// limit: every CU runs nothing but MFMAs (fp16, or fp32 for the f32_ mixes)
+// on operands held in registers
 // (2 waves per SIMD, as version 7), back to back for a settle phase and then
 // 20 timed launches, while the driver's metrics table is sampled
 // (libvk_bench.so).  One JSON line per operand mix:
@@ -20,17 +21,22 @@
 //            operand register (A, or B at a row change) the previous one
 //            ended on
 //   *_w1     the same mix with one wave per SIMD (256-thread workgroups)
+//   f32_32x32x2  v_mfma_f32_32x32x2_f32 rotating over 8 accumulators of 16
+//            registers (fp32 operands, one register each), as fp32 version 2
+//   f32_16x16x4  v_mfma_f32_16x16x4_f32 rotating over 16 accumulators
 //
 // No GEMM reaches more than its mix's figure on the same board: the figure
 // prices the MFMA work alone, with no loads, LDS traffic or barriers.
 //
-//   vibekernel_amd/harness/bin/mfma_stream [settle_ms]
+//   vibekernel_amd/harness/bin/mfma_stream [settle_ms [mix,mix,...]]
 #include <hip/hip_runtime.h>
 
 #include <chrono>
 #include <cstdio>
 #include <cstdlib>
+#include <cstring>
 #include <random>
+#include <string>
 #include <vector>
 
 #include "playground/utils.hpp"
@@ -54,7 +60,50 @@ __global__ __launch_bounds__(kThreads) void mfma_stream(const half8* __restrict_
     b[i] = src[t * 8 + 4 + i];
   }
   float s = 0.0f;
-  if constexpr (kMode == 2) {
+  if constexpr (kMode == 7 || kMode == 8) {
+    // fp32 operands: one register each, 4 per lane of A and of B
+    float af[4], bf[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      af[i] = (float)a[i][0] + (float)a[i][1];
+      bf[i] = (float)b[i][0] + (float)b[i][1];
+    }
+    if constexpr (kMode == 7) {
+      float16v acc[8];
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) acc[j][r] = 0.0f;
+      for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int r = 0; r < 4; r++)
+#pragma unroll
+          for (int j = 0; j < 8; j++) {
+            acc[j] = __builtin_amdgcn_mfma_f32_32x32x2f32(af[(j + r) & 3], bf[j & 3], acc[j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; j++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) s += acc[j][r];
+    } else {
+      float4v acc[16];
+#pragma unroll
+      for (int j = 0; j < 16; j++) acc[j] = float4v{0.0f, 0.0f, 0.0f, 0.0f};
+      for (int it = 0; it < iters; it++) {
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+          for (int j = 0; j < 16; j++) {
+            acc[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[(j + r) & 3], bf[j >> 2], acc[j], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+      }
+#pragma unroll
+      for (int j = 0; j < 16; j++) s += acc[j][0] + acc[j][1] + acc[j][2] + acc[j][3];
+    }
+  } else if constexpr (kMode == 2) {
     float16v acc[4];
 #pragma unroll
     for (int j = 0; j < 4; j++)
@@ -127,10 +176,12 @@ struct Mix {
   double flop_per_mfma;
   int mfma_per_iter;  // per wave
   int threads;        // per workgroup (one per CU): 512 = 2 waves per SIMD, 256 = 1
+  double flop_clk_cu = 4096.0;  // dense peak per clock per CU (fp16 4096, fp32 256)
 };
 
 int main(int argc, char** argv) {
   const double settle_ms = argc > 1 ? std::atof(argv[1]) : 2500.0;
+  const std::string only = argc > 2 ? std::string(",") + argv[2] + "," : std::string();
   int dev = 0, cus = 0;
   PLAYGROUND_HIP_CHECK(hipGetDevice(&dev));
   PLAYGROUND_HIP_CHECK(hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev));
@@ -162,6 +213,10 @@ int main(int argc, char** argv) {
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsPin));
   PLAYGROUND_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_stream<6>),
                                            hipFuncAttributeMaxDynamicSharedMemorySize, kLdsPin));
+  PLAYGROUND_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_stream<7>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsPin));
+  PLAYGROUND_HIP_CHECK(hipFuncSetAttribute(reinterpret_cast<const void*>(mfma_stream<8>),
+                                           hipFuncAttributeMaxDynamicSharedMemorySize, kLdsPin));
 
   constexpr double k16 = 16.0 * 16 * 32 * 2;
   const Mix mixes[] = {{"chain2", 0, false, k16, 32, 512},    {"rotate", 1, false, k16, 32, 512},
@@ -169,11 +224,14 @@ int main(int argc, char** argv) {
                        {"zero", 0, true, k16, 32, 512},      {"chain4", 3, false, k16, 64, 512},
                        {"chain8", 4, false, k16, 128, 512},  {"gemm", 5, false, k16, 32, 512},
                        {"snake", 6, false, k16, 32, 512},    {"chain2_w1", 0, false, k16, 32, 256},
-                       {"rotate_w1", 1, false, k16, 32, 256}, {"snake_w1", 6, false, k16, 32, 256}};
+                       {"rotate_w1", 1, false, k16, 32, 256}, {"snake_w1", 6, false, k16, 32, 256},
+                       {"f32_32x32x2", 7, false, 32.0 * 32 * 2 * 2, 32, 512, 256.0},
+                       {"f32_16x16x4", 8, false, 16.0 * 16 * 4 * 2, 32, 512, 256.0}};
   for (const Mix& mx : mixes) {
+    if (!only.empty() && only.find(std::string(",") + mx.name + ",") == std::string::npos) continue;
     const half8* src = mx.zero ? d_zero : d_rand;
     // about 1 ms per launch at the full rate
-    const int iters = (mx.mode == 2 ? 1024 : 2048) * 32 / mx.mfma_per_iter;
+    const int iters = (mx.mode == 2 || mx.mode >= 7 ? 1024 : 2048) * 32 / mx.mfma_per_iter;
     // 96 KB of (unused) dynamic LDS per workgroup: one workgroup per CU
     auto launch = [&]() {
       if (mx.mode == 0)
@@ -188,8 +246,12 @@ int main(int argc, char** argv) {
         hipLaunchKernelGGL(mfma_stream<4>, dim3(grid), dim3(mx.threads), kLdsPin, 0, src, d_out, iters);
       else if (mx.mode == 5)
         hipLaunchKernelGGL(mfma_stream<5>, dim3(grid), dim3(mx.threads), kLdsPin, 0, src, d_out, iters);
-      else
+      else if (mx.mode == 6)
         hipLaunchKernelGGL(mfma_stream<6>, dim3(grid), dim3(mx.threads), kLdsPin, 0, src, d_out, iters);
+      else if (mx.mode == 7)
+        hipLaunchKernelGGL(mfma_stream<7>, dim3(grid), dim3(mx.threads), kLdsPin, 0, src, d_out, iters);
+      else
+        hipLaunchKernelGGL(mfma_stream<8>, dim3(grid), dim3(mx.threads), kLdsPin, 0, src, d_out, iters);
     };
     bool sampling = false;
     const auto t0 = std::chrono::steady_clock::now();
@@ -227,9 +289,10 @@ int main(int argc, char** argv) {
       const vkb_clock_sample& s = smp[(ns < 64 ? ns : 64) - 1];  // the last refresh before the timed launches
       std::printf(", \"sclk_mhz\": %.1f, \"socket_w\": %.1f, \"xcd_mhz\": [", s.gfx_mhz, s.socket_w);
       for (int x = 0; x < 8; x++) std::printf("%s%.0f", x ? ", " : "", s.xcd_mhz[x]);
-      std::printf("], \"frac_of_peak_at_sclk\": %.4f", tflops / (cus * 4096.0 * s.gfx_mhz * 1e6 / 1e12));
+      std::printf("], \"frac_of_peak_at_sclk\": %.4f", tflops / (cus * mx.flop_clk_cu * s.gfx_mhz * 1e6 / 1e12));
     }
-    std::printf(", \"frac_of_2516.6\": %.4f}\n", tflops / 2516.6);
+    const double spec = cus * mx.flop_clk_cu * 2.4e9 / 1e12;  // 2516.6 (fp16) or 157.3 (fp32) on 256 CUs
+    std::printf(", \"frac_of_spec_peak\": %.4f, \"spec_peak_tflops\": %.1f}\n", tflops / spec, spec);
     std::fflush(stdout);
   }
   PLAYGROUND_HIP_CHECK(hipFree(d_rand));

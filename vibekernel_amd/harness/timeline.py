@@ -1,5 +1,6 @@
 #!/usr/bin/env python3
-"""Per-workgroup timeline of version 7 (measurement tool).
+"""Per-workgroup timeline of version 7, or of version 8 with --skinny
+(measurement tool).
 
 Loads the timeline build of the library (`make -C vibekernel_amd/csrc
 timeline` -> vibekernel_amd/lib/libvk_gemm_timeline.so, where version 7's
@@ -23,6 +24,13 @@ XCD.  Prints one JSON object:
 
     python vibekernel_amd/harness/timeline.py [--m 4096 --n 4096 --k 4096]
 
+With --skinny (default shape 16 x 8192 x 8192) version 8's workgroups record
+their XCD, k part, k-steps and the clock at entry, at the end of the k-loop
+and when they leave; by_xcd then gives each XCD's mean and latest k-loop
+end and the B bytes its workgroups streamed per microsecond of k-loop.
+
+    python vibekernel_amd/harness/timeline.py --skinny [--m 16 --n 8192 --k 8192]
+
 Not part of the product path: the timeline build exists for this tool only.
 """
 from __future__ import annotations
@@ -40,14 +48,20 @@ LIB = os.path.join(HERE, "..", "lib")
 
 def main() -> int:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
-    p.add_argument("--m", type=int, default=4096)
-    p.add_argument("--n", type=int, default=4096)
-    p.add_argument("--k", type=int, default=4096)
+    p.add_argument("--skinny", action="store_true", help="version 8 (default shape 16 x 8192 x 8192)")
+    p.add_argument("--dump", default=None, help="with --skinny: write every workgroup's record to this file")
+    p.add_argument("--m", type=int, default=None)
+    p.add_argument("--n", type=int, default=None)
+    p.add_argument("--k", type=int, default=None)
     p.add_argument("--settle-ms", type=float, default=2500.0)
     p.add_argument("--seed", type=int, default=20261201)
     a = p.parse_args()
-    m, n, k = a.m, a.n, a.k
-    if m % 256 or n % 256 or k % 64:
+    dm, dn, dk = (16, 8192, 8192) if a.skinny else (4096, 4096, 4096)
+    m, n, k = a.m or dm, a.n or dn, a.k or dk
+    if a.skinny and (m > 256 or n % 128 or k % 32):
+        print("timeline.py: --skinny takes M <= 256, N a multiple of 128 and K of 32", file=sys.stderr)
+        return 2
+    if not a.skinny and (m % 256 or n % 256 or k % 64):
         print("timeline.py: version 7 needs M, N multiples of 256 and K of 64", file=sys.stderr)
         return 2
 
@@ -67,6 +81,8 @@ def main() -> int:
     T.vk_gemm.restype = ctypes.c_int
     T.vk_timeline_read.argtypes = [vp, ctypes.c_int]
     T.vk_timeline_read.restype = ctypes.c_int
+    T.vk_timeline_sk_read.argtypes = [vp, ctypes.c_int]
+    T.vk_timeline_sk_read.restype = ctypes.c_int
     sys.path.insert(0, os.path.join(HERE, "..", ".."))
     import bench as B  # the clock sampler bindings (libvk_bench.so)
 
@@ -79,7 +95,7 @@ def main() -> int:
     Bm = (torch.rand((k, n), generator=g, device=dev) * 2 - 1).half()
     C = torch.empty((m, n), dtype=torch.float16, device=dev)
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    args = (7, 1, 1, m, n, k, ctypes.c_void_p(A.data_ptr()), ctypes.c_void_p(Bm.data_ptr()),
+    args = (8 if a.skinny else 7, 1, 1, m, n, k, ctypes.c_void_p(A.data_ptr()), ctypes.c_void_p(Bm.data_ptr()),
             ctypes.c_void_p(C.data_ptr()), s)
 
     def run(count):
@@ -105,6 +121,8 @@ def main() -> int:
     if sampling:
         clock.stop()
     near = min(samples, key=lambda x: abs(x.t_ms - t_start)) if samples else None
+    if a.skinny:
+        return skinny_report(T, a, m, n, k, e0, e1, near, t_start)
 
     groups = (m // 256) * (n // 256)
     rec = min(groups, 4096)
@@ -145,6 +163,62 @@ def main() -> int:
             "cycles_per_ktile": round(cyc, 1) if cyc else None,
             "loop_mfma_efficiency": round(2048.0 / cyc, 4) if cyc else None,
         })
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def skinny_report(T, a, m, n, k, e0, e1, near, t_start) -> int:
+    """Version 8's records: (entry, k-loop end, leave, XCD, k-steps, k part)."""
+    import numpy as np
+
+    nc = 128  # columns per workgroup (f16_skinny_sk.hip pick_nc)
+    groups = -(-n // nc)
+    ks = 1
+    while ks < 8 and groups * ks * 2 <= 256 and k // 32 // (ks * 2) >= 4:
+        ks *= 2
+    rec = min(groups * ks, 4096)
+    buf = np.zeros(rec * 6, dtype=np.uint64)
+    if T.vk_timeline_sk_read(buf.ctypes.data, rec) != 0:
+        print("timeline.py: vk_timeline_sk_read failed", file=sys.stderr)
+        return 1
+    r = buf.reshape(rec, 6)
+    ts = r[:, :3].astype(np.float64) / 100.0  # 100 MHz ticks -> us
+    ts -= ts[:, 0].min()
+    xcc, steps, part = r[:, 3].astype(int), r[:, 4].astype(int), r[:, 5].astype(int)
+    bbytes = steps * 32 * nc * 2  # B bytes each workgroup streamed
+    loop = ts[:, 1] - ts[:, 0]
+    out = {
+        "workload": f"gemm_f16_{m}x{n}x{k} version 8 (timeline build), uniform[-1,1) seed {a.seed}",
+        "event_us_per_launch": round(e0.elapsed_time(e1) * 1e3 / 20, 2),
+        "workgroups": int(rec), "k_parts": ks,
+        "span_us": round(float(ts[:, 2].max()), 2),
+        "loop_end_us_min_mean_max": [round(float(f(ts[:, 1])), 2) for f in (np.min, np.mean, np.max)],
+        "leave_after_loop_us_mean_max": [round(float(f(ts[:, 2] - ts[:, 1])), 2) for f in (np.mean, np.max)],
+        "sclk_sample_age_ms": round(near.t_ms - t_start, 1) if near else None,
+        "by_xcd": [], "by_part": [],
+    }
+    for x in range(8):
+        sel = xcc == x
+        if not sel.any():
+            continue
+        out["by_xcd"].append({
+            "xcd": x, "sclk_mhz": float(near.xcd_mhz[x]) if near else None, "workgroups": int(sel.sum()),
+            "entry_us_mean_max": [round(float(ts[sel, 0].mean()), 2), round(float(ts[sel, 0].max()), 2)],
+            "loop_us_mean_max": [round(float(loop[sel].mean()), 2), round(float(loop[sel].max()), 2)],
+            "loop_end_us_mean": round(float(ts[sel, 1].mean()), 2),
+            "loop_end_us_max": round(float(ts[sel, 1].max()), 2),
+            "b_gb_per_s_per_workgroup": round(float((bbytes[sel] / loop[sel]).mean()) / 1e3, 2),
+            "b_tb_per_s_of_xcd": round(float(bbytes[sel].sum() / ts[sel, 1].max()) / 1e6, 3),
+        })
+    for q in range(ks):
+        sel = part == q
+        out["by_part"].append({"part": q, "steps": int(steps[sel].max()) if sel.any() else 0,
+                               "xcds": sorted(set(int(v) for v in xcc[sel])),
+                               "loop_us_mean": round(float(loop[sel].mean()), 2) if sel.any() else None,
+                               "loop_end_us_mean": round(float(ts[sel, 1].mean()), 2) if sel.any() else None})
+    if a.dump:
+        np.savetxt(a.dump, np.column_stack([ts, xcc, steps, part]), fmt="%.3f %.3f %.3f %d %d %d",
+                   header="entry_us loop_end_us leave_us xcd steps part")
     print(json.dumps(out), flush=True)
     return 0
 
