@@ -5,10 +5,11 @@ Measured on MI355X with tests/golden/lds_bank_probe.hip (one wave, 16
 instances of one LDS instruction per dispatch, SQ_LDS_BANK_CONFLICT under
 rocprofv3; fixture tests/golden/lds_bank_probe_gfx950.json):
 
-* the banks are 64 x 4 bytes: two accesses conflict when their addresses
+* reads see 64 banks of 4 bytes: two reads conflict when their addresses
   differ by a multiple of 256 bytes (for 16-byte accesses: the same 16-byte
   slot, address / 16 mod 16), and only if the hardware serves them in the
-  same pass;
+  same pass; writes see the banks repeat every 128 bytes (two writes of one
+  pass conflict when their addresses differ by a multiple of 128 bytes);
 * ds_read_b128 is served in 4 passes of 16 lanes: lane l is in pass
   (l / 32, parity of bits 2-4 of l) -- not 16 consecutive lanes;
 * ds_read_b64 in 2 passes of 32 consecutive lanes, ds_write_b128 in 8
@@ -19,7 +20,10 @@ The probe's two-lane patterns fix the pass of every lane; its whole-wave
 patterns (the kernels' own fragment reads) check the cycle count.  Under
 this model version 8's A fragment reads with chunk ^ (row / 4) % 4 take 8
 cycles instead of 4 (the 25-33 % conflict share its counters showed), and
-chunk ^ (row / 2) % 4, the kernel's layout, takes 4."""
+chunk ^ (row / 2) % 4, the kernel's layout, takes 4; version 11's epilogue
+staging writes with units ^ 2 ((row / 4) % 4) (fp16) and chunks ^
+(row / 2) % 8 (fp32) took 4 and 8 conflict cycles each (all of that
+kernel's conflicts), and the kernel's layouts take none."""
 import json
 import os
 import re
@@ -45,15 +49,17 @@ PASS_OF = {
     "wr64": lambda l: l >> 4,
 }
 SLOT_BYTES = {"rd128": 16, "rd64": 8, "wr128": 16, "wr64": 8}
+BANK_PERIOD = {"rd128": 256, "rd64": 256, "wr128": 128, "wr64": 128}
 
 
 def conflict_cycles(op, addrs, lanes=range(64)):
     """Cycles beyond one per pass: in each pass, the distinct addresses on
-    its most-used slot (address mod 256 in SLOT_BYTES units), minus one."""
-    sb = SLOT_BYTES[op]
+    its most-used slot (address mod BANK_PERIOD in SLOT_BYTES units), minus
+    one."""
+    sb, period = SLOT_BYTES[op], BANK_PERIOD[op]
     passes = {}
     for l in lanes:
-        passes.setdefault(PASS_OF[op](l), {}).setdefault((addrs[l] % 256) // sb, set()).add(addrs[l] // sb)
+        passes.setdefault(PASS_OF[op](l), {}).setdefault((addrs[l] % period) // sb, set()).add(addrs[l] // sb)
     return sum(max(len(v) for v in slots.values()) - 1 for slots in passes.values())
 
 
@@ -83,6 +89,97 @@ def test_rd128_model_matches_whole_wave_patterns(probe):
         conf, active = measured[label]
         assert active == 4 + conf, label  # 4 passes plus the conflict cycles
         assert conflict_cycles("rd128", [f(l) for l in range(64)]) == conf, label
+
+
+@pytest.mark.parametrize("op,period", [("rd128", 256), ("rd64", 256), ("rdtr64", 256), ("wr128", 128), ("wr64", 128)])
+def test_bank_period_matches_the_offset_sweeps(probe, op, period):
+    """Lanes (0, b) of one pass, lane b at offset X: a conflict exactly when X
+    is a multiple of the bank period (256 bytes for reads, 128 for writes)."""
+    sweep = probe["xsweep_" + op]
+    assert len(sweep) >= 192
+    for b, x, conf in sweep:
+        # ds_read_b64_tr_b16 (no pass model here) pairs lane 0 with every
+        # swept lane up to 32
+        same_pass = op == "rdtr64" or PASS_OF[op](b) == PASS_OF[op](0)
+        assert conf == (1.0 if same_pass and x % period == 0 else 0.0), (op, b, x, conf)
+
+
+def test_write_model_matches_whole_wave_patterns(probe):
+    funcs = {"wr64 v7epiH j=0": ("wr64", lambda l: pat.v7_epi_h(l, 0, 0)),
+             "wr64 v7epiH j=1": ("wr64", lambda l: pat.v7_epi_h(l, 0, 1)),
+             "wr128 v7epiF j=0": ("wr128", lambda l: pat.v7_epi_f(l, 0, 0)),
+             "wr128 v7epiF j=1": ("wr128", lambda l: pat.v7_epi_f(l, 0, 1)),
+             "wr64 v3epiH j=0 g4=0": ("wr64", lambda l: pat.v3_epi_h(l, 0, 0, 0)),
+             "wr64 linear": ("wr64", lambda l: 8 * l), "wr128 linear": ("wr128", lambda l: 16 * l)}
+    for name, f in pat.V11_EPI_H.items():
+        for j in (0, 1):
+            funcs[f"wr64 v11epiH {name} j={j}"] = ("wr64", lambda l, f=f, j=j: pat.v11_epi_h(l, 0, j, f))
+    for name, f in pat.V11_EPI_F.items():
+        for j in (0, 1):
+            funcs[f"wr128 v11epiF {name} j={j}"] = ("wr128", lambda l, f=f, j=j: pat.v11_epi_f(l, 0, j, f))
+        funcs[f"rd128 v11epiFread {name} q=0"] = ("rd128", lambda l, f=f: pat.v11_epi_f_read(l, 0, f))
+    passes = {"wr64": 4, "wr128": 8, "rd128": 4}
+    measured = {p[0]: (p[1], p[2]) for p in probe["patterns"]}
+    for label, (op, f) in funcs.items():
+        conf, active = measured[label]
+        assert active == passes[op] + conf, label
+        assert conflict_cycles(op, [f(l) for l in range(64)]) == conf, label
+    # the layouts version 11 had: every pass of every write takes two cycles
+    assert measured["wr64 v11epiH swz 2((r>>2)&3) j=0"][0] == 4
+    assert measured["wr128 v11epiF swz (r>>1)&7 j=0"][0] == 8
+
+
+def _v11_epilogue_swizzles():
+    src = open(os.path.join(ROOT, "vibekernel_amd", "csrc", "f16_pp128.hip")).read()
+    h = re.search(r"struct Epi<half_t> \{.*?int swz\(int row\) \{ return \(row >> 1\) & 7; \}", src, re.S)
+    f = re.findall(r"16 \* \((?:chunk|ch) \^ \(row & 7\)\)", src)
+    assert h, "Epi<half_t>::swz is not (row >> 1) & 7"
+    assert len(f) == 3, "Epi<float> stage and both reads must use chunk ^ (row & 7)"
+    return (lambda r: (r >> 1) & 7), (lambda r: r & 7)
+
+
+def test_version11_epilogue_conflict_free():
+    """Version 11's (and 12's, 13's) staging of C: every write and read of
+    both output types is conflict-free under the model, and the reads
+    return what the writes put (fp16: a read's 8-byte halves swapped when
+    (row / 2) is odd)."""
+    sh, sf = _v11_epilogue_swizzles()
+    for i in range(4):
+        for j in range(2):
+            assert conflict_cycles("wr64", [pat.v11_epi_h(l, i, j, sh) for l in range(64)]) == 0
+            assert conflict_cycles("wr128", [pat.v11_epi_f(l, i, j, sf) for l in range(64)]) == 0
+    for q in range(4):
+        rows = [16 * q + (l >> 2) for l in range(64)]
+        addrs = [r * 64 + 16 * ((l & 3) ^ (sh(r) >> 1)) for l, r in zip(range(64), rows)]
+        assert conflict_cycles("rd128", addrs) == 0
+    for q in range(8):
+        assert conflict_cycles("rd128", [pat.v11_epi_f_read(l, q, sf) for l in range(64)]) == 0
+    # round trip at 8-byte-unit granularity (fp16) and 16-byte chunks (fp32)
+    lds = {}
+    for i in range(4):
+        for j in range(2):
+            for l in range(64):
+                lds[pat.v11_epi_h(l, i, j, sh)] = (16 * i + (l & 15), 4 * j + (l >> 4))
+    for q in range(4):
+        for l in range(64):
+            row, ch = 16 * q + (l >> 2), l & 3
+            base = row * 64 + 16 * (ch ^ (sh(row) >> 1))
+            lo, hi = lds[base], lds[base + 8]
+            if sh(row) & 1:
+                lo, hi = hi, lo
+            assert (lo, hi) == ((row, 2 * ch), (row, 2 * ch + 1))
+    lds = {}
+    for i in range(4):
+        for j in range(2):
+            for l in range(64):
+                lds[pat.v11_epi_f(l, i, j, sf)] = (16 * i + (l & 15), 4 * j + (l >> 4))
+    for q in range(8):
+        for l in range(64):
+            assert lds[pat.v11_epi_f_read(l, q, sf)] == (8 * q + (l >> 3), l & 7)
+    # the previous layouts fail the model, as the probe measured
+    old_h, old_f = pat.V11_EPI_H["swz 2((r>>2)&3)"], pat.V11_EPI_F["swz (r>>1)&7"]
+    assert conflict_cycles("wr64", [pat.v11_epi_h(l, 0, 0, old_h) for l in range(64)]) == 4
+    assert conflict_cycles("wr128", [pat.v11_epi_f(l, 0, 0, old_f) for l in range(64)]) == 8
 
 
 def test_consecutive_lane_passes_would_not_explain_the_measurements(probe):

@@ -76,15 +76,22 @@ template <typename OutT>
 struct Epi;
 
 // fp16: rows of 64 B = 8 units of 8 B (4 halves); unit u of row r at
-// u ^ 2 ((r / 4) % 4).  Rows 4 apart share banks; a write instruction's
-// 32-lane half names 16 rows x 2 unit columns, and the XOR (which keeps
-// unit bit 0) puts them on 8 distinct units per bank class: two passes per
-// instruction, the least its 512 bytes take.  A read takes units 2c, 2c+1
-// (16 B) at the unit pair c ^ (r / 4) % 4.
+// u ^ (r / 2) % 8.  gfx950 serves a ds_write_b64 in passes of 16 lanes over
+// banks that repeat every 128 bytes (measured: two lanes of a pass whose
+// addresses differ by a multiple of 128 B take two cycles).  A pass names 16
+// consecutive rows of one unit column, two rows per 128 bytes: the XOR puts
+// the 8 rows of each parity on 8 distinct units, one cycle per pass.  A read
+// takes units 2c, 2c+1 (16 B) from the slot c ^ (r / 4) % 4, its two 8-byte
+// halves swapped when (r / 2) is odd.
 template <>
 struct Epi<half_t> {
   static constexpr int kRegion = 64 * 64;
-  static __device__ __forceinline__ int swz(int row) { return ((row >> 2) & 3) << 1; }
+  static __device__ __forceinline__ int swz(int row) { return (row >> 1) & 7; }
+  static __device__ __forceinline__ uint4v read_pair(uint32_t wbase, int row, int ch) {
+    const uint4v v = lds_read16(wbase + row * 64 + 16 * (ch ^ (swz(row) >> 1)));
+    const bool odd = swz(row) & 1;
+    return uint4v{odd ? v[2] : v[0], odd ? v[3] : v[1], odd ? v[0] : v[2], odd ? v[1] : v[3]};
+  }
   static __device__ __forceinline__ void stage(uint32_t wbase, int lane, int i, int j, const float4v& v) {
     const int row = 16 * i + (lane & 15), unit = 4 * j + (lane >> 4);
     half4 h = {(half_t)v[0], (half_t)v[1], (half_t)v[2], (half_t)v[3]};
@@ -96,7 +103,7 @@ struct Epi<half_t> {
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const int row = 16 * q + rsub;
-      const uint4v v = lds_read16(wbase + row * 64 + 16 * (ch ^ (swz(row) >> 1)));
+      const uint4v v = read_pair(wbase, row, ch);
       store_out16(cr, (uint32_t)(row * N + ch * 8) * 2u, v);
     }
   }
@@ -111,20 +118,22 @@ struct Epi<half_t> {
 #pragma unroll
     for (int q = 0; q < 4; q++) {
       const int row = 16 * q + rsub;
-      const uint4v v = lds_read16(wbase + row * 64 + 16 * (ch ^ (swz(row) >> 1)));
+      const uint4v v = read_pair(wbase, row, ch);
       if (col_in && row0 + row < M) *reinterpret_cast<uint4v*>(C + (size_t)(row0 + row) * N + col0 + ch * 8) = v;
     }
   }
 };
 
 // fp32: rows of 128 B = 8 chunks of 16 B (4 floats); chunk u of row r at
-// u ^ (r / 2) % 8.
+// u ^ r % 8.  A ds_write_b128 pass (8 lanes: 8 consecutive rows of one chunk
+// column) then covers the 8 chunk positions of the 128-byte bank period, and
+// a read (8 rows x 8 chunks) the 16 slots of each of its passes.
 template <>
 struct Epi<float> {
   static constexpr int kRegion = 64 * 128;
   static __device__ __forceinline__ void stage(uint32_t wbase, int lane, int i, int j, const float4v& v) {
     const int row = 16 * i + (lane & 15), chunk = 4 * j + (lane >> 4);
-    lds_write16(wbase + row * 128 + 16 * (chunk ^ ((row >> 1) & 7)), v);
+    lds_write16(wbase + row * 128 + 16 * (chunk ^ (row & 7)), v);
   }
   static __device__ __forceinline__ void store(uint32_t wbase, float* Cw, int N, int lane) {
     const int rsub = lane >> 3, ch = lane & 7;
@@ -132,7 +141,7 @@ struct Epi<float> {
 #pragma unroll
     for (int q = 0; q < 8; q++) {
       const int row = 8 * q + rsub;
-      const uint4v v = lds_read16(wbase + row * 128 + 16 * (ch ^ ((row >> 1) & 7)));
+      const uint4v v = lds_read16(wbase + row * 128 + 16 * (ch ^ (row & 7)));
       store_out16(cr, (uint32_t)(row * N + ch * 4) * 4u, v);
     }
   }
@@ -143,7 +152,7 @@ struct Epi<float> {
 #pragma unroll
     for (int q = 0; q < 8; q++) {
       const int row = 8 * q + rsub;
-      const uint4v v = lds_read16(wbase + row * 128 + 16 * (ch ^ ((row >> 1) & 7)));
+      const uint4v v = lds_read16(wbase + row * 128 + 16 * (ch ^ (row & 7)));
       if (col_in && row0 + row < M) *reinterpret_cast<uint4v*>(C + (size_t)(row0 + row) * N + col0 + ch * 4) = v;
     }
   }
