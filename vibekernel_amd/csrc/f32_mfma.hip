@@ -1,30 +1,36 @@
-// f32_mfma.hip -- fp32 GEMM on the matrix cores (version 2 for fp32).
+// f32_mfma.hip -- fp32 GEMM on the matrix cores (versions 2 and 3 for fp32).
 //
 // Same operator as fp32 version 1 (f32_valu.hip: the harness's fp32 path,
 // results/naive_cycle4/include/playground/system.hpp:35-41, ground truth
 // matmul_f32_v0_cblas.cpp:8-12), computed with v_mfma_f32_32x32x2_f32.
-// Measured on MI355X with random operands on all CUs (2 waves per SIMD,
-// harness/mfma_stream): that instruction over 8 accumulators in rotation
-// sustains 153.3 TFLOP/s (0.983 of the 157.3 dense fp32 figure at the
-// measured 2.38 GHz; fp32 MFMAs stay below the board's power limit) and the
-// 16x16x4 form 152.7; a 16x16x4 version of this kernel measured slower.  An
-// fp32 MFMA
-// does 64 FLOP per clock per SIMD -- 16x fewer than the fp16 form -- so the
-// operand traffic per cycle is small and the kernel can be simple:
-//  * 256x256 tile, 8 waves; wave w owns rows 128*(w/4) .. +127 and columns
-//    64*(w%4) .. +63: 4x2 blocks of 32x32 (128 fp32 accumulators per lane);
-//  * BK-deep k-tiles (A 256xBK and B BKx256 fp32) in an LDS ring filled by
-//    direct-to-LDS loads, one barrier per k-tile: BK = 32 in 2 stages of 64 KB
-//    when K allows, else BK = 16 in 4 stages of 32 KB;
-//  * per k-tile each wave reads its fragments (BK/2 ds_read_b128 of A, BK
-//    ds_read_b32 of B) and issues 4*BK MFMAs of 64 cycles, with its loads of
-//    a later k-tile going out one after each of the first MFMA steps.
-// Fragments: the MFMA takes lane l's A value as X[l%32][l/32] and its B value
-// as Y[l/32][l%32] (2 k per instruction).  Step s of a k-tile pairs k = s
-// (lanes 0..31) with k = BK/2 + s (lanes 32..63), so a lane's A values for
-// the BK/2 steps are BK/2 consecutive k of one row (16-byte reads) and its B
-// values one column of BK/2 k-rows.  Result: lane l, register r holds
-// D[8*(r/4) + 4*(l/32) + r%4][l%32] of the block.
+// Measured on MI355X with random operands on all CUs (harness/mfma_stream):
+// that instruction over 8 accumulators in rotation sustains 153.3-154.1
+// TFLOP/s (0.983-0.986 of the 157.3 dense fp32 figure at the measured
+// 2.38 GHz) with two waves per SIMD and 153.8 (0.984) with one; fp32 MFMAs
+// stay below the board's power limit, so cycles are time.  The 16x16x4 form
+// reaches 152.7 / 150.9 and a 16x16x4 version of this kernel measured
+// slower.  An fp32 MFMA does 64 FLOP per clock per SIMD -- 16x fewer than
+// the fp16 form -- so the operand traffic per cycle is small and no
+// ping-pong is needed.  Common to both kernels below:
+//  * 256x256 tiles; BK-deep k-tiles (A 256xBK and B BKx256 fp32) in an LDS
+//    ring filled by direct-to-LDS loads, one barrier per k-tile;
+//  * fragments: the MFMA takes lane l's A value as X[l%32][l/32] and its B
+//    value as Y[l/32][l%32] (2 k per instruction).  Step s of a k-tile pairs
+//    k = s (lanes 0..31) with k = BK/2 + s (lanes 32..63), so a lane's A
+//    values for the BK/2 steps are BK/2 consecutive k of one row (16-byte
+//    reads) and its B values one column of BK/2 k-rows.  Result: lane l,
+//    register r holds D[8*(r/4) + 4*(l/32) + r%4][l%32] of the block;
+//  * per element the sum runs over the steps in ascending order, k-tile by
+//    k-tile, so the two kernels give the same bits.
+// Version 2 with K % 32 == 0 runs the four-wave kernel (f32_mfma4_kernel:
+// one wave per SIMD owning a 128x128 quarter, 32-deep k-tiles in 2 stages of
+// 64 KB); version 3 (masked edges) and version 2 with K % 32 == 16 run the
+// eight-wave kernel (f32_mfma_kernel: wave w owns rows 128*(w/4) and columns
+// 64*(w%4) onward, 4x2 blocks of 32x32; BK = 32 in 2 stages, or 16 in 4
+// stages of 32 KB).  The four-wave form measured 0.8-1.4 % faster at
+// 4096^3 (and -0.8 % at 4096 x 4096 x 8192), the eight-wave form 0.6-1.0 %
+// faster with masked edges (4000^3, 1000 x 3000 x 2000), all interleaved on
+// one box.
 // LDS swizzles (physical 16-byte chunk = logical ^ f(row)):
 //  * A rows are 4*BK bytes: f = (row / 4) % 4 for 64-byte rows, (row / 2) % 8
 //    for 128-byte rows, so 16 consecutive rows reading one logical chunk hit
@@ -44,7 +50,7 @@ namespace vk {
 namespace {
 
 constexpr int kBM = 256, kBN = 256;
-constexpr int kThreads = 512;
+constexpr int kThreads = 512;  // the eight-wave kernel
 
 // k-tile depth BK (fp32): 16 with a 4-stage ring or 32 with 2 stages (128 KB
 // of LDS either way).
@@ -56,8 +62,8 @@ struct F32Cfg {
   static constexpr int kStageBytes = kABytes + kBBytes;
   static constexpr int kLdsBytes = kNS * kStageBytes;
   static constexpr int kRowChunks = BK / 4;     // 16-byte chunks per A row
-  static constexpr int kDmaA = BK / 8;          // A instructions per wave per k-tile
-  static constexpr int kDmaB = BK / 8;          // B instructions per wave per k-tile
+  static constexpr int kDmaA = BK / 8;          // A instructions per wave per k-tile (eight waves)
+  static constexpr int kDmaB = BK / 8;          // B instructions per wave per k-tile (eight waves)
   static constexpr int kDma = kDmaA + kDmaB;
   static constexpr int kSteps = BK / 2;         // MFMA k-steps per k-tile
   static_assert(kLdsBytes <= 160 * 1024, "LDS budget");
@@ -86,6 +92,10 @@ __device__ __forceinline__ float4v lds_read_f4(uint32_t addr) {
   return *reinterpret_cast<const __attribute__((address_space(3))) float4v*>(addr);
 }
 
+// Eight-wave kernel: per k-tile each wave reads its fragments (BK/2
+// ds_read_b128 of A, BK ds_read_b32 of B) and issues 4*BK MFMAs of 64
+// cycles, with its loads of a later k-tile going out one after each of the
+// first MFMA steps.
 // kEdge (version 3): the tiles may reach past M rows or N columns and the
 // last k-tile past K (any M; N, K multiples of 4).  The loads then go through
 // buffer resources over the whole matrices, the k-tile's offset in the
@@ -272,6 +282,275 @@ __global__ __launch_bounds__(kThreads) void f32_mfma_kernel(const float* __restr
       }
 }
 
+// Timeline build (make timeline -> libvk_gemm_timeline.so, VK_TIMELINE=1):
+// every wave of the first 1024 workgroups of the four-wave kernel records
+// the 100 MHz real-time clock at entry, at the start and end of its k-loop
+// and after its C stores complete, its XCD, and in shader clock cycles the
+// k-loop's length and the part of it spent from the last group's first
+// MFMA step to the end of the k-tile barrier (waits for this wave's LDS reads
+// and loads, and the barrier); vk_timeline_f32_read() copies them out.  The
+// product library is built with VK_TIMELINE=0 and records nothing.
+#ifndef VK_TIMELINE
+#define VK_TIMELINE 0
+#endif
+#if VK_TIMELINE
+constexpr int kF32TimelineWaves = 1024 * 4;
+__device__ unsigned long long vk_timeline_f32[kF32TimelineWaves * 8];
+extern "C" int vk_timeline_f32_read(unsigned long long* host, int waves) {
+  if (waves < 0 || waves > kF32TimelineWaves) return -3;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(vk_timeline_f32), sizeof(unsigned long long) * 8 * waves, 0,
+                             hipMemcpyDeviceToHost) == hipSuccess ? 0 : -7;
+}
+#endif
+
+// Four-wave kernel (version 2, K % 32 == 0): the eight-wave kernel's tile,
+// 32-deep k-tiles, LDS layout, loads and per-element k order, with one wave
+// per SIMD owning a 128x128 quarter (4x4 blocks of 32x32: 256 fp32
+// accumulators per lane in AGPRs); wave w owns rows 128*(w/2) and columns
+// 128*(w%2) onward.  Per k-tile a wave reads 16 KB of A and 16 KB of B
+// fragments (the eight-wave kernel's waves 16 + 8 KB each, two per SIMD):
+// a third less LDS data per MFMA.  Its fragments are read one group of 4
+// steps ahead into a second register set, one read after each of the first
+// 12 MFMAs of the group's second step; the k-tile's one barrier sits after
+// the first step of its last group (whose fragments are already in
+// registers), followed by the next k-tile's first group of reads and, one
+// after every third MFMA of the last three steps, the 16 loads that refill
+// the slot just freed with k-tile t + 2 (clamped to the last k-tile: a
+// refill past the end rewrites the last k-tile's data into a slot nobody
+// reads).  Measured per k-tile (timeline build, 4096^3): 17,113 shader
+// cycles against the 16,384 its MFMAs need on every XCD (0.957); instrumented
+// copies without the fragment reads took 16,420 (the A reads' 16
+// ds_read_b128 cost ~510 cycles, the B reads' 32 ds_read2st64_b32 ~225),
+// without the loads 16,988, without the barrier 17,090.
+__global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict__ A, const float* __restrict__ B,
+                                                        float* __restrict__ C, int M, int N, int K) {
+  constexpr int BK = 32;
+  using G = F32Cfg<BK>;
+  constexpr int kDA = 2 * G::kDmaA, kDB = 2 * G::kDmaB, kD = kDA + kDB;  // 8 + 8 loads per wave per k-tile
+  static_assert(kD == 16, "one load per MFMA of a step");
+  extern __shared__ __attribute__((aligned(1024))) char lds[];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int wr = wave >> 1, wc = wave & 1;
+  int tm, tn;
+  tile_of(blockIdx.x, M / kBM, N / kBN, tm, tn);
+  const int m0 = tm * kBM, n0 = tn * kBN;
+  const uint32_t lds_base = lds_addr32(lds);
+
+#if VK_TIMELINE
+  const unsigned long long tl_entry = __builtin_amdgcn_s_memrealtime();
+  unsigned long long tl_bar = 0;
+#endif
+  // Load d < 8 of a wave is A instruction 8 w + d (8 rows of 128 bytes),
+  // load 8 + e its B instruction 8 w + e (the k-row of that number, 1 KB).
+  constexpr int kRowsPerDma = 1024 / (4 * BK);
+  uint32_t voffA[kDA], voffB[kDB];
+#pragma unroll
+  for (int d = 0; d < kDA; d++) {
+    const int i = kDA * wave + d;
+    const int row = kRowsPerDma * i + lane / G::kRowChunks;
+    const int ca = (lane % G::kRowChunks) ^ swz_a32<BK>(row);
+    voffA[d] = (uint32_t)(((size_t)row * K + ca * 4) * 4);
+  }
+#pragma unroll
+  for (int d = 0; d < kDB; d++) {
+    const int i = kDB * wave + d;
+    const int cb = lane ^ swz_b32<BK>(i);
+    voffB[d] = (uint32_t)(((size_t)i * N + cb * 4) * 4);
+  }
+  const char* gA = reinterpret_cast<const char*>(A) + (size_t)m0 * K * 4;
+  const char* gB = reinterpret_cast<const char*>(B) + (size_t)n0 * 4;
+  auto issue_one = [&](int kt, int slot, int d) {
+    const uint32_t s = lds_base + slot * G::kStageBytes;
+    if (d < kDA)
+      dma16(gA + (size_t)kt * BK * 4, voffA[d], s + (kDA * wave + d) * 1024);
+    else
+      dma16(gB + (size_t)kt * BK * N * 4, voffB[d - kDA], s + G::kABytes + (kDB * wave + d - kDA) * 1024);
+  };
+
+  const int h = lane >> 5;
+  uint32_t aoff[4][4];
+#pragma unroll
+  for (int bi = 0; bi < 4; bi++) {
+    const int row = wr * 128 + bi * 32 + (lane & 31);
+#pragma unroll
+    for (int c = 0; c < 4; c++) aoff[bi][c] = row * (4 * BK) + 16 * ((4 * h + c) ^ swz_a32<BK>(row));
+  }
+  uint32_t boff[4];
+#pragma unroll
+  for (int bj = 0; bj < 4; bj++) {
+    const int col = wc * 128 + bj * 32 + (lane & 31);
+    boff[bj] = G::kABytes + G::kSteps * h * 1024 + 16 * ((col >> 2) ^ (h << 3)) + 4 * (col & 3);
+  }
+
+  float16v_ acc[4][4];
+#pragma unroll
+  for (int bi = 0; bi < 4; bi++)
+#pragma unroll
+    for (int bj = 0; bj < 4; bj++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) acc[bi][bj][r] = 0.0f;
+  prefer_agpr_accumulators();
+
+  struct Frag {
+    float a[4][4];  // [block][step of the group]
+    float b[4][4];
+  };
+  Frag f[2];
+  auto read_group = [&](Frag& fr, uint32_t s, auto gc) {
+    constexpr int g = decltype(gc)::value;
+#pragma unroll
+    for (int bi = 0; bi < 4; bi++) {
+      const float4v v = lds_read_f4(s + aoff[bi][g]);
+#pragma unroll
+      for (int q = 0; q < 4; q++) fr.a[bi][q] = v[q];
+    }
+#pragma unroll
+    for (int bj = 0; bj < 4; bj++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) fr.b[bj][q] = lds_read_f32(s + boff[bj] + (4 * g + q) * 1024);
+  };
+  // Read i of a group (0..11): the 16-byte A read of block i (i < 4), else
+  // the two B values of block (i - 4) / 2, steps 2 ((i - 4) % 2) and + 1.
+  auto read_one = [&](Frag& fr, uint32_t s, int g, int i) {
+    if (i < 4) {
+      const float4v v = lds_read_f4(s + aoff[i][g]);
+#pragma unroll
+      for (int q = 0; q < 4; q++) fr.a[i][q] = v[q];
+    } else {
+      const int bj = (i - 4) >> 1, q = 2 * ((i - 4) & 1);
+      fr.b[bj][q] = lds_read_f32(s + boff[bj] + (4 * g + q) * 1024);
+      fr.b[bj][q + 1] = lds_read_f32(s + boff[bj] + (4 * g + q + 1) * 1024);
+    }
+  };
+  auto mfma_step = [&](const Frag& fr, int q) {
+#pragma unroll
+    for (int bi = 0; bi < 4; bi++)
+#pragma unroll
+      for (int bj = 0; bj < 4; bj++)
+        acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(fr.a[bi][q], fr.b[bj][q], acc[bi][bj], 0, 0, 0);
+  };
+
+  const int nk = K / BK;
+  // Prologue: k-tiles 0 and 1 (clamped) in flight, k-tile 0 waited for.
+#pragma unroll
+  for (int d = 0; d < kD; d++) issue_one(0, 0, d);
+#pragma unroll
+  for (int d = 0; d < kD; d++) issue_one(min(1, nk - 1), 1, d);
+  wait_vmcnt<kD>();
+  lds_barrier();
+  read_group(f[0], lds_base, std::integral_constant<int, 0>{});
+#if VK_TIMELINE
+  const unsigned long long tl_loop_rt = __builtin_amdgcn_s_memrealtime();
+  const unsigned long long tl_loop_c = __builtin_amdgcn_s_memtime();
+#endif
+
+  for (int t = 0; t < nk; t++) {
+    const uint32_t s = lds_base + (t & 1) * G::kStageBytes;
+    static_for<4>([&](auto gc) {
+      constexpr int g = decltype(gc)::value;
+#if VK_TIMELINE
+      unsigned long long tl_b0 = 0;
+      if constexpr (g == 3) tl_b0 = __builtin_amdgcn_s_memtime();
+#endif
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_step(f[g & 1], 0);
+      __builtin_amdgcn_sched_barrier(0);
+      if constexpr (g < 3) {
+        // step 1, the next group's 12 reads one after each of its first MFMAs
+#pragma unroll
+        for (int bi = 0; bi < 4; bi++)
+#pragma unroll
+          for (int bj = 0; bj < 4; bj++) {
+            const int m = 4 * bi + bj;
+            acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(f[g & 1].a[bi][1], f[g & 1].b[bj][1], acc[bi][bj], 0, 0, 0);
+            if (m < 12) {
+              __builtin_amdgcn_sched_barrier(0);
+              read_one(f[(g + 1) & 1], s, g + 1, m);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+          }
+      } else {
+        wait_lgkmcnt0();
+        wait_vmcnt<0>();  // this wave's loads of k-tile t + 1
+        lds_barrier();    // everyone's; also ends every read of slot t & 1
+#if VK_TIMELINE
+        tl_bar += __builtin_amdgcn_s_memtime() - tl_b0;
+#endif
+        const uint32_t s_next = lds_base + ((t + 1) & 1) * G::kStageBytes;
+        const int kt_next = min(t + 2, nk - 1);
+        // steps 1..3 (48 MFMAs): the next k-tile's first 12 reads after the
+        // first 12, a load after every third, A and B alternating
+#pragma unroll
+        for (int q = 1; q < 4; q++)
+#pragma unroll
+          for (int bi = 0; bi < 4; bi++)
+#pragma unroll
+            for (int bj = 0; bj < 4; bj++) {
+              const int m = 16 * (q - 1) + 4 * bi + bj;
+              __builtin_amdgcn_sched_barrier(0);
+              acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(f[1].a[bi][q], f[1].b[bj][q], acc[bi][bj], 0, 0, 0);
+              if (m < 12) {
+                __builtin_amdgcn_sched_barrier(0);
+                read_one(f[0], s_next, 0, m);
+              }
+              if (m % 3 == 0 && m / 3 < kD) {
+                const int d = m / 3;
+                __builtin_amdgcn_sched_barrier(0);
+                issue_one(kt_next, t & 1, (d & 1) ? kDA + (d >> 1) : (d >> 1));
+              }
+            }
+      }
+      if constexpr (g < 3) {
+        __builtin_amdgcn_sched_barrier(0);
+        mfma_step(f[g & 1], 2);
+        mfma_step(f[g & 1], 3);
+      }
+    });
+  }
+  wait_vmcnt<0>();  // clamped refills past the last k-tile
+#if VK_TIMELINE
+  const unsigned long long tl_end_c = __builtin_amdgcn_s_memtime();
+  const unsigned long long tl_end_rt = __builtin_amdgcn_s_memrealtime();
+#endif
+
+  const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const int row0 = m0 + wr * 128, col0 = n0 + wc * 128;
+#pragma unroll
+  for (int bi = 0; bi < 4; bi++)
+#pragma unroll
+    for (int bj = 0; bj < 4; bj++)
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        const int row = row0 + bi * 32 + 8 * (r >> 2) + 4 * (lane_e >> 5) + (r & 3);
+        const int col = col0 + bj * 32 + (lane_e & 31);
+        C[(size_t)row * N + col] = acc[bi][bj][r];
+      }
+#if VK_TIMELINE
+  wait_vmcnt0_ordered();
+  const unsigned long long tl_exit = __builtin_amdgcn_s_memrealtime();
+  const int rec = (int)blockIdx.x * 4 + wave;
+  if (lane == 0 && rec < kF32TimelineWaves) {
+    unsigned xcc;
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    unsigned long long* r = vk_timeline_f32 + rec * 8;
+    r[0] = tl_entry; r[1] = tl_loop_rt; r[2] = tl_end_rt; r[3] = tl_exit; r[4] = xcc & 15u;
+    r[5] = tl_end_c - tl_loop_c; r[6] = tl_bar; r[7] = (unsigned long long)nk;
+  }
+#endif
+}
+
+hipError_t launch_f32_mfma4(const GemmArgs& a) {
+  static std::atomic<uint64_t> attr_done{0};
+  auto kfn = f32_mfma4_kernel;
+  hipError_t e = ensure_lds_attr(kfn, F32Cfg<32>::kLdsBytes, a.device, attr_done);
+  if (e != hipSuccess) return e;
+  const int tiles = (int)((a.m / kBM) * (a.n / kBN));
+  hipLaunchKernelGGL(kfn, dim3(tiles), dim3(256), F32Cfg<32>::kLdsBytes, a.stream, static_cast<const float*>(a.A),
+                     static_cast<const float*>(a.B), static_cast<float*>(a.C), (int)a.m, (int)a.n, (int)a.k);
+  return hipGetLastError();
+}
+
 // 32-deep k-tiles when K allows (one barrier per 128 MFMAs of a wave:
 // measured 141.2 against 139.6 TFLOP/s at 4096^3), else 16-deep.
 template <int BK, bool kEdge = false>
@@ -287,7 +566,7 @@ hipError_t launch_bk(const GemmArgs& a) {
   return hipGetLastError();
 }
 
-hipError_t launch_f32_mfma(const GemmArgs& a) { return a.k % 32 == 0 ? launch_bk<32>(a) : launch_bk<16>(a); }
+hipError_t launch_f32_mfma(const GemmArgs& a) { return a.k % 32 == 0 ? launch_f32_mfma4(a) : launch_bk<16>(a); }
 
 // 32-bit lane offsets: the rows of A one instruction covers span less than
 // 256 * K floats beyond the k-tile base and the k-rows of B 32 * N floats;
@@ -313,7 +592,7 @@ void register_f32_mfma() {
   e.version = 2;
   e.in_dtype = VK_DTYPE_F32;
   e.name = "f32_v2_mfma256";
-  e.caps = make_caps(2, VK_DTYPE_F32, kOutF32, kBM, kBN, 16, 16, kBM, kBN, 32, kThreads, F32Cfg<32>::kLdsBytes, 0, 0);
+  e.caps = make_caps(2, VK_DTYPE_F32, kOutF32, kBM, kBN, 16, 16, kBM, kBN, 32, 256, F32Cfg<32>::kLdsBytes, 0, 0);
   e.launch = launch_f32_mfma;
   e.workspace = nullptr;
   e.shape_ok = f32_mfma_shape_ok;

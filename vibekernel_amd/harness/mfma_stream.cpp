@@ -24,6 +24,7 @@
 //   f32_32x32x2  v_mfma_f32_32x32x2_f32 rotating over 8 accumulators of 16
 //            registers (fp32 operands, one register each), as fp32 version 2
 //   f32_16x16x4  v_mfma_f32_16x16x4_f32 rotating over 16 accumulators
+//   f32_*_w1 the fp32 mixes with one wave per SIMD
 //
 // No GEMM reaches more than its mix's figure on the same board: the figure
 // prices the MFMA work alone, with no loads, LDS traffic or barriers.
@@ -226,7 +227,9 @@ int main(int argc, char** argv) {
                        {"snake", 6, false, k16, 32, 512},    {"chain2_w1", 0, false, k16, 32, 256},
                        {"rotate_w1", 1, false, k16, 32, 256}, {"snake_w1", 6, false, k16, 32, 256},
                        {"f32_32x32x2", 7, false, 32.0 * 32 * 2 * 2, 32, 512, 256.0},
-                       {"f32_16x16x4", 8, false, 16.0 * 16 * 4 * 2, 32, 512, 256.0}};
+                       {"f32_16x16x4", 8, false, 16.0 * 16 * 4 * 2, 32, 512, 256.0},
+                       {"f32_32x32x2_w1", 7, false, 32.0 * 32 * 2 * 2, 32, 256, 256.0},
+                       {"f32_16x16x4_w1", 8, false, 16.0 * 16 * 4 * 2, 32, 256, 256.0}};
   for (const Mix& mx : mixes) {
     if (!only.empty() && only.find(std::string(",") + mx.name + ",") == std::string::npos) continue;
     const half8* src = mx.zero ? d_zero : d_rand;

@@ -31,6 +31,14 @@ end and the B bytes its workgroups streamed per microsecond of k-loop.
 
     python vibekernel_amd/harness/timeline.py --skinny [--m 16 --n 8192 --k 8192]
 
+With --f32 (default 4096^3) fp32 version 2's four-wave kernel: every wave
+records its XCD, the clock at entry, k-loop start and end and after its
+stores complete, and in shader-clock cycles its k-loop and the part spent
+from each k-tile's last group to the end of its barrier; the report gives
+cycles per 32-deep k-tile against the 16384 a SIMD's MFMAs need.
+
+    python vibekernel_amd/harness/timeline.py --f32 [--m 4096 --n 4096 --k 4096]
+
 Not part of the product path: the timeline build exists for this tool only.
 """
 from __future__ import annotations
@@ -49,6 +57,8 @@ LIB = os.path.join(HERE, "..", "lib")
 def main() -> int:
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--skinny", action="store_true", help="version 8 (default shape 16 x 8192 x 8192)")
+    p.add_argument("--f32", action="store_true", help="fp32 version 2, four-wave kernel (default shape 4096^3)")
+    p.add_argument("--lib", default=None, help="the timeline build to load (default vibekernel_amd/lib/libvk_gemm_timeline.so)")
     p.add_argument("--dump", default=None, help="with --skinny: write every workgroup's record to this file")
     p.add_argument("--m", type=int, default=None)
     p.add_argument("--n", type=int, default=None)
@@ -61,7 +71,10 @@ def main() -> int:
     if a.skinny and (m > 256 or n % 128 or k % 32):
         print("timeline.py: --skinny takes M <= 256, N a multiple of 128 and K of 32", file=sys.stderr)
         return 2
-    if not a.skinny and (m % 256 or n % 256 or k % 64):
+    if a.f32 and (m % 256 or n % 256 or k % 32 or (m // 256) * (n // 256) > 1024):
+        print("timeline.py: --f32 needs M, N multiples of 256 (at most 1024 tiles) and K of 32", file=sys.stderr)
+        return 2
+    if not a.skinny and not a.f32 and (m % 256 or n % 256 or k % 64):
         print("timeline.py: version 7 needs M, N multiples of 256 and K of 64", file=sys.stderr)
         return 2
 
@@ -71,7 +84,7 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("timeline.py: no GPU visible", file=sys.stderr)
         return 1
-    path = os.path.join(LIB, "libvk_gemm_timeline.so")
+    path = a.lib or os.path.join(LIB, "libvk_gemm_timeline.so")
     if not os.path.exists(path):
         print(f"timeline.py: {path} is missing (make -C vibekernel_amd/csrc timeline)", file=sys.stderr)
         return 1
@@ -83,6 +96,8 @@ def main() -> int:
     T.vk_timeline_read.restype = ctypes.c_int
     T.vk_timeline_sk_read.argtypes = [vp, ctypes.c_int]
     T.vk_timeline_sk_read.restype = ctypes.c_int
+    T.vk_timeline_f32_read.argtypes = [vp, ctypes.c_int]
+    T.vk_timeline_f32_read.restype = ctypes.c_int
     sys.path.insert(0, os.path.join(HERE, "..", ".."))
     import bench as B  # the clock sampler bindings (libvk_bench.so)
 
@@ -91,12 +106,14 @@ def main() -> int:
 
     dev = torch.device("cuda:0")
     g = torch.Generator(device=dev).manual_seed(a.seed)
-    A = (torch.rand((m, k), generator=g, device=dev) * 2 - 1).half()
-    Bm = (torch.rand((k, n), generator=g, device=dev) * 2 - 1).half()
-    C = torch.empty((m, n), dtype=torch.float16, device=dev)
+    dt = torch.float32 if a.f32 else torch.float16
+    A = (torch.rand((m, k), generator=g, device=dev) * 2 - 1).to(dt)
+    Bm = (torch.rand((k, n), generator=g, device=dev) * 2 - 1).to(dt)
+    C = torch.empty((m, n), dtype=dt, device=dev)
     s = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-    args = (8 if a.skinny else 7, 1, 1, m, n, k, ctypes.c_void_p(A.data_ptr()), ctypes.c_void_p(Bm.data_ptr()),
-            ctypes.c_void_p(C.data_ptr()), s)
+    dcode = 2 if a.f32 else 1  # vk_dtype: 1 fp16, 2 fp32
+    args = (2 if a.f32 else 8 if a.skinny else 7, dcode, dcode, m, n, k, ctypes.c_void_p(A.data_ptr()),
+            ctypes.c_void_p(Bm.data_ptr()), ctypes.c_void_p(C.data_ptr()), s)
 
     def run(count):
         for _ in range(count):
@@ -123,6 +140,8 @@ def main() -> int:
     near = min(samples, key=lambda x: abs(x.t_ms - t_start)) if samples else None
     if a.skinny:
         return skinny_report(T, a, m, n, k, e0, e1, near, t_start)
+    if a.f32:
+        return f32_report(T, a, m, n, k, e0, e1, near, t_start)
 
     groups = (m // 256) * (n // 256)
     rec = min(groups, 4096)
@@ -219,6 +238,55 @@ def skinny_report(T, a, m, n, k, e0, e1, near, t_start) -> int:
     if a.dump:
         np.savetxt(a.dump, np.column_stack([ts, xcc, steps, part]), fmt="%.3f %.3f %.3f %d %d %d",
                    header="entry_us loop_end_us leave_us xcd steps part")
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+def f32_report(T, a, m, n, k, e0, e1, near, t_start) -> int:
+    """fp32 version 2's records per wave: (entry, loop start, loop end, stores
+    complete, XCD, loop cycles, last-group-and-barrier cycles, k-tiles)."""
+    import numpy as np
+
+    waves = (m // 256) * (n // 256) * 4
+    buf = np.zeros(waves * 8, dtype=np.uint64)
+    if T.vk_timeline_f32_read(buf.ctypes.data, waves) != 0:
+        print("timeline.py: vk_timeline_f32_read failed", file=sys.stderr)
+        return 1
+    r = buf.reshape(waves, 8)
+    ts = r[:, :4].astype(np.float64) / 100.0  # 100 MHz ticks -> us
+    ts -= ts[:, 0].min()
+    xcc = r[:, 4].astype(int)
+    loop_c, bar_c, nk = r[:, 5].astype(np.float64), r[:, 6].astype(np.float64), r[:, 7].astype(np.float64)
+    loop_us = ts[:, 2] - ts[:, 1]
+    ideal = 256 * 64.0  # one wave per SIMD: 256 MFMAs of 64 cycles per k-tile
+    out = {
+        "workload": f"gemm_f32_{m}x{n}x{k} fp32 version 2, four-wave kernel (timeline build), seed {a.seed}",
+        "event_us_per_launch": round(e0.elapsed_time(e1) * 1e3 / 20, 2),
+        "span_us": round(float(ts[:, 3].max()), 2),
+        "entry_skew_us_max": round(float(ts[:, 0].max()), 2),
+        "prologue_us": round(float((ts[:, 1] - ts[:, 0]).mean()), 2),
+        "loop_us_mean": round(float(loop_us.mean()), 2),
+        "loop_end_us_min_mean_max": [round(float(f(ts[:, 2])), 2) for f in (np.min, np.mean, np.max)],
+        "epilogue_us_mean_max": [round(float(f(ts[:, 3] - ts[:, 2])), 2) for f in (np.mean, np.max)],
+        "memtime_mhz": round(float((loop_c / loop_us).mean()), 1),
+        "cycles_per_ktile": round(float((loop_c / nk).mean()), 1),
+        "last_group_and_barrier_cycles_per_ktile": round(float((bar_c / nk).mean()), 1),
+        "loop_mfma_efficiency": round(float((ideal * nk / loop_c).mean()), 4),
+        "sclk_sample_age_ms": round(near.t_ms - t_start, 1) if near else None,
+        "by_xcd": [],
+    }
+    for x in range(8):
+        sel = xcc == x
+        if not sel.any():
+            continue
+        out["by_xcd"].append({
+            "xcd": x, "sclk_mhz": float(near.xcd_mhz[x]) if near else None, "waves": int(sel.sum()),
+            "loop_us_mean": round(float(loop_us[sel].mean()), 2),
+            "loop_end_us_max": round(float(ts[sel, 2].max()), 2),
+            "exit_us_max": round(float(ts[sel, 3].max()), 2),
+            "cycles_per_ktile": round(float((loop_c[sel] / nk[sel]).mean()), 1),
+            "last_group_and_barrier_cycles_per_ktile": round(float((bar_c[sel] / nk[sel]).mean()), 1),
+        })
     print(json.dumps(out), flush=True)
     return 0
 
