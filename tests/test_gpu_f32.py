@@ -3,9 +3,11 @@
 
 * version 1 (VALU, one fmaf per term in ascending k): equal to the oracle,
   bit for bit, on every shape;
-* version 2 (matrix cores, v_mfma_f32_32x32x2_f32, two products per step):
-  integer inputs exact; random inputs within 2 k u |A||B| of the exact
-  (fp64) product; bitwise repeatable launch to launch;
+* version 2 (matrix cores, v_mfma_f32_32x32x2_f32, two products per step;
+  the four-wave kernel when K % 32 == 0, the eight-wave one with 16-deep
+  k-tiles otherwise): integer inputs exact; random inputs within 2 k u
+  |A||B| of the exact (fp64) product; bitwise repeatable launch to launch;
+  shapes include one k-tile (K = 32) and more tiles than CUs;
 * version 3 (version 2 with masked edges: any M, N and K multiples of 4): the
   same bars on ragged shapes, bitwise equal to version 2 on its grid, nothing
   written outside C, and the values past an edge in memory never reach C.
@@ -19,7 +21,8 @@ pytestmark = pytest.mark.gpu
 
 SHAPES_V1 = [(128, 128, 16), (256, 384, 64), (512, 512, 512), (1, 1, 1), (17, 33, 65), (130, 250, 70),
              (128, 256, 16), (256, 512, 32), (384, 768, 48), (1024, 512, 1024), (128, 256, 2000)]
-SHAPES_V2 = [(256, 256, 16), (512, 256, 64), (256, 512, 48), (768, 512, 256), (1024, 1024, 512)]
+SHAPES_V2 = [(256, 256, 16), (512, 256, 64), (256, 512, 48), (768, 512, 256), (1024, 1024, 512), (256, 256, 32),
+             (4352, 4096, 64)]
 SHAPES_V3 = [(1, 4, 4), (17, 36, 68), (300, 260, 100), (257, 512, 36), (1000, 1000, 1000), (256, 256, 64)]
 CASES = [(1, s) for s in SHAPES_V1] + [(2, s) for s in SHAPES_V2] + [(3, s) for s in SHAPES_V3]
 
@@ -114,7 +117,7 @@ def test_f32_mfma_rejects_unaligned_shape(gpu):
 def test_f32_edge_on_grid_equals_v2(gpu):
     """On version 2's grid with K % 32 == 0 both run 32-deep k-tiles in the
     same order: bitwise equal."""
-    for m, n, k in [(256, 256, 64), (512, 768, 320)]:
+    for m, n, k in [(256, 256, 64), (512, 768, 320), (256, 512, 32)]:
         A, B = make_inputs(m, n, k, "normal", seed=m + k, dtype=np.float32)
         assert np.array_equal(_run(A, B, 2).view(np.uint32), _run(A, B, 3).view(np.uint32))
 
