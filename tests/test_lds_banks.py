@@ -182,6 +182,45 @@ def test_version11_epilogue_conflict_free():
     assert conflict_cycles("wr128", [pat.v11_epi_f(l, 0, 0, old_f) for l in range(64)]) == 8
 
 
+def test_versions_2_3_epilogue_conflict_free():
+    """Versions 2/3 stage a wave's 128 x 128 fp16 block in 256-byte rows:
+    8-byte unit u of row r at u ^ (r % 16) (the kernel's form, read from
+    the source), so each ds_write_b64 pass of 16 consecutive rows covers the
+    16 unit positions of the 128-byte write period; the reads (4 rows x 16
+    slots, halves swapped for odd rows) stay conflict-free and return what
+    was written.  The previous 16-byte-chunk form, measured at 4 conflict
+    cycles per write, fails the model."""
+    src = open(os.path.join(ROOT, "vibekernel_amd", "csrc", "f16_dma.hip")).read()
+    assert "row * 256 + 8 * ((2 * chunk + hsel) ^ (row & 15))" in src
+    assert "row * 256 + 16 * (ch ^ ((row & 15) >> 1))" in src
+
+    def wr(l, i, j, g4):
+        row, u = 32 * i + (l & 31), 2 * (4 * j + g4) + (l >> 5)
+        return row * 256 + 8 * (u ^ (row & 15))
+
+    def rd(l, q):
+        row, ch = 4 * q + (l >> 4), l & 15
+        return row * 256 + 16 * (ch ^ ((row & 15) >> 1))
+
+    lds = {}
+    for i in range(4):
+        for j in range(4):
+            for g4 in range(4):
+                addrs = [wr(l, i, j, g4) for l in range(64)]
+                assert conflict_cycles("wr64", addrs) == 0
+                for l in range(64):
+                    lds[addrs[l]] = (32 * i + (l & 31), 2 * (4 * j + g4) + (l >> 5))
+    for q in range(32):
+        assert conflict_cycles("rd128", [rd(l, q) for l in range(64)]) == 0
+        for l in range(64):
+            row, ch = 4 * q + (l >> 4), l & 15
+            lo, hi = lds[rd(l, q)], lds[rd(l, q) + 8]
+            if row & 1:
+                lo, hi = hi, lo
+            assert (lo, hi) == ((row, 2 * ch), (row, 2 * ch + 1))
+    assert conflict_cycles("wr64", [pat.v3_epi_h(l, 0, 0, 0) for l in range(64)]) == 4
+
+
 def test_consecutive_lane_passes_would_not_explain_the_measurements(probe):
     """The obvious model (passes of 16 consecutive lanes) calls version 8's
     old A layout conflict-free, which the probe contradicts: the pass

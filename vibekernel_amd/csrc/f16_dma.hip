@@ -56,8 +56,14 @@ struct Cfg {
 // block; fp32: half of it per pass).
 constexpr int kEpiWaveBytes = 128 * 128 * 2;
 
-// fp16 output: the wave's 128x128 block, row pitch 256 B = 16 chunks of 16 B,
-// physical chunk = chunk ^ (row % 16).  Read back 4 rows per instruction.
+// fp16 output: the wave's 128x128 block, row pitch 256 B = 32 units of 8 B
+// (4 halves), physical unit = unit ^ (row % 16).  A ds_write_b64 pass (16
+// lanes: 16 consecutive rows of one unit) then covers the 16 unit positions
+// of the 128-byte period in which LDS writes see the banks repeat (units
+// chunk ^ (row % 16) at 16-byte granularity cost 4 conflict cycles per
+// write).  A read takes units 2ch, 2ch+1 (16 B) from the 16-byte slot
+// ch ^ (row % 16) / 2, its two halves swapped for odd rows; 4 rows per
+// instruction.
 template <typename OutT>
 __device__ __forceinline__ typename std::enable_if<std::is_same<OutT, half_t>::value>::type
 epilogue_store(float16v (&acc)[4][4], char*, uint32_t wbase, OutT* Cw, int N, int lane) {
@@ -72,13 +78,15 @@ epilogue_store(float16v (&acc)[4][4], char*, uint32_t wbase, OutT* Cw, int N, in
         const int chunk = 4 * j + g4;
         half4 h = {(half_t)acc[i][j][4 * g4 + 0], (half_t)acc[i][j][4 * g4 + 1],
                    (half_t)acc[i][j][4 * g4 + 2], (half_t)acc[i][j][4 * g4 + 3]};
-        lds_write8(wbase + row * 256 + 16 * (chunk ^ (row & 15)) + 8 * hsel, h);
+        lds_write8(wbase + row * 256 + 8 * ((2 * chunk + hsel) ^ (row & 15)), h);
       }
   const int rsub = lane >> 4, ch = lane & 15;
 #pragma unroll
   for (int q = 0; q < 32; q++) {
     const int row = 4 * q + rsub;
-    const uint4v v = lds_read16(wbase + row * 256 + 16 * (ch ^ (row & 15)));
+    const uint4v u = lds_read16(wbase + row * 256 + 16 * (ch ^ ((row & 15) >> 1)));
+    const bool odd = row & 1;
+    const uint4v v = {odd ? u[2] : u[0], odd ? u[3] : u[1], odd ? u[0] : u[2], odd ? u[1] : u[3]};
     *reinterpret_cast<uint4v*>(Cw + (size_t)row * N + ch * 8) = v;
   }
 }
