@@ -8,9 +8,10 @@
   k-tiles otherwise): integer inputs exact; random inputs within 2 k u
   |A||B| of the exact (fp64) product; bitwise repeatable launch to launch;
   shapes include one k-tile (K = 32) and more tiles than CUs;
-* version 3 (version 2 with masked edges: any M, N and K multiples of 4): the
-  same bars on ragged shapes, bitwise equal to version 2 on its grid, nothing
-  written outside C, and the values past an edge in memory never reach C.
+* version 3 (version 2 with masked edges: any M, N and K multiples of 4; the
+  four-wave kernel when K % 32 == 0): the same bars on ragged shapes,
+  bitwise equal to version 2 on its grid, nothing written outside C, and the
+  values past an edge in memory never reach C.
 """
 import numpy as np
 import pytest
@@ -23,7 +24,8 @@ SHAPES_V1 = [(128, 128, 16), (256, 384, 64), (512, 512, 512), (1, 1, 1), (17, 33
              (128, 256, 16), (256, 512, 32), (384, 768, 48), (1024, 512, 1024), (128, 256, 2000)]
 SHAPES_V2 = [(256, 256, 16), (512, 256, 64), (256, 512, 48), (768, 512, 256), (1024, 1024, 512), (256, 256, 32),
              (4352, 4096, 64)]
-SHAPES_V3 = [(1, 4, 4), (17, 36, 68), (300, 260, 100), (257, 512, 36), (1000, 1000, 1000), (256, 256, 64)]
+SHAPES_V3 = [(1, 4, 4), (17, 36, 68), (300, 260, 100), (257, 512, 36), (1000, 1000, 1000), (256, 256, 64),
+             (300, 260, 96), (257, 516, 64), (1000, 1000, 1024), (1, 4, 32)]
 CASES = [(1, s) for s in SHAPES_V1] + [(2, s) for s in SHAPES_V2] + [(3, s) for s in SHAPES_V3]
 
 
@@ -122,7 +124,7 @@ def test_f32_edge_on_grid_equals_v2(gpu):
         assert np.array_equal(_run(A, B, 2).view(np.uint32), _run(A, B, 3).view(np.uint32))
 
 
-@pytest.mark.parametrize("shape", [(300, 260, 100), (1, 4, 4), (600, 36, 1028)])
+@pytest.mark.parametrize("shape", [(300, 260, 100), (1, 4, 4), (600, 36, 1028), (300, 260, 128), (600, 36, 1024)])
 def test_f32_edge_writes_only_c(gpu, shape):
     import torch
     import vibekernel_amd as vk

@@ -22,15 +22,17 @@
 //    register r holds D[8*(r/4) + 4*(l/32) + r%4][l%32] of the block;
 //  * per element the sum runs over the steps in ascending order, k-tile by
 //    k-tile, so the two kernels give the same bits.
-// Version 2 with K % 32 == 0 runs the four-wave kernel (f32_mfma4_kernel:
-// one wave per SIMD owning a 128x128 quarter, 32-deep k-tiles in 2 stages of
-// 64 KB); version 3 (masked edges) and version 2 with K % 32 == 16 run the
-// eight-wave kernel (f32_mfma_kernel: wave w owns rows 128*(w/4) and columns
-// 64*(w%4) onward, 4x2 blocks of 32x32; BK = 32 in 2 stages, or 16 in 4
-// stages of 32 KB).  The four-wave form measured 0.8-1.4 % faster at
-// 4096^3 (and -0.8 % at 4096 x 4096 x 8192), the eight-wave form 0.6-1.0 %
-// faster with masked edges (4000^3, 1000 x 3000 x 2000), all interleaved on
-// one box.
+// Versions 2 and 3 with K % 32 == 0 run the four-wave kernel
+// (f32_mfma4_kernel: one wave per SIMD owning a 128x128 quarter, 32-deep
+// k-tiles in 2 stages of 64 KB; for version 3 with buffer loads and bounded
+// stores); other K run the eight-wave kernel (f32_mfma_kernel: wave w owns
+// rows 128*(w/4) and columns 64*(w%4) onward, 4x2 blocks of 32x32; version
+// 2 with K % 32 == 16: BK = 16 in 4 stages of 32 KB; version 3: BK = 32 in
+// 2 stages, the last k-tile masked per lane).  Interleaved on one box, the
+// four-wave form measured 0.8-1.4 % faster at 4096^3 (0.8 % at 4096 x 4096
+// x 8192) and with edges 1.1 % at 4000^3 and 0.7 % at 1000 x 3000 x 2048;
+// with the last k-tile's per-lane masking as well (64-bit mask shifts
+// between the MFMAs) it was 0.6-1.0 % slower than the eight-wave form.
 // LDS swizzles (physical 16-byte chunk = logical ^ f(row)):
 //  * A rows are 4*BK bytes: f = (row / 4) % 4 for 64-byte rows, (row / 2) % 8
 //    for 128-byte rows, so 16 consecutive rows reading one logical chunk hit
@@ -303,7 +305,7 @@ extern "C" int vk_timeline_f32_read(unsigned long long* host, int waves) {
 }
 #endif
 
-// Four-wave kernel (version 2, K % 32 == 0): the eight-wave kernel's tile,
+// Four-wave kernel (versions 2 and 3, K % 32 == 0): the eight-wave kernel's tile,
 // 32-deep k-tiles, LDS layout, loads and per-element k order, with one wave
 // per SIMD owning a 128x128 quarter (4x4 blocks of 32x32: 256 fp32
 // accumulators per lane in AGPRs); wave w owns rows 128*(w/2) and columns
@@ -322,6 +324,7 @@ extern "C" int vk_timeline_f32_read(unsigned long long* host, int waves) {
 // copies without the fragment reads took 16,420 (the A reads' 16
 // ds_read_b128 cost ~510 cycles, the B reads' 32 ds_read2st64_b32 ~225),
 // without the loads 16,988, without the barrier 17,090.
+template <bool kEdge>
 __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                         float* __restrict__ C, int M, int N, int K) {
   constexpr int BK = 32;
@@ -333,7 +336,7 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wr = wave >> 1, wc = wave & 1;
   int tm, tn;
-  tile_of(blockIdx.x, M / kBM, N / kBN, tm, tn);
+  tile_of(blockIdx.x, (M + (kEdge ? kBM - 1 : 0)) / kBM, (N + (kEdge ? kBN - 1 : 0)) / kBN, tm, tn);
   const int m0 = tm * kBM, n0 = tn * kBN;
   const uint32_t lds_base = lds_addr32(lds);
 
@@ -360,12 +363,29 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
   }
   const char* gA = reinterpret_cast<const char*>(A) + (size_t)m0 * K * 4;
   const char* gB = reinterpret_cast<const char*>(B) + (size_t)n0 * 4;
+  const uint32_t sizeA = kEdge ? (uint32_t)M * (uint32_t)K * 4u : 0u;
+  const uint32_t sizeB = kEdge ? (uint32_t)K * (uint32_t)N * 4u : 0u;
+  const __amdgpu_buffer_rsrc_t rsrcA =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(A), 0, (int)sizeA, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rsrcB =
+      __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(B), 0, (int)sizeB, kBufferWord3);
   auto issue_one = [&](int kt, int slot, int d) {
     const uint32_t s = lds_base + slot * G::kStageBytes;
-    if (d < kDA)
-      dma16(gA + (size_t)kt * BK * 4, voffA[d], s + (kDA * wave + d) * 1024);
-    else
-      dma16(gB + (size_t)kt * BK * N * 4, voffB[d - kDA], s + G::kABytes + (kDB * wave + d - kDA) * 1024);
+    if constexpr (kEdge) {
+      // K % 32 == 0: only rows past M and columns past N; the buffer ranges
+      // give zeros past each matrix (B columns past N read the next row's,
+      // feeding only C columns that are not stored)
+      if (d < kDA)
+        dma16_buf(rsrcA, voffA[d], (uint32_t)(m0 * K + kt * BK) * 4u, s + (kDA * wave + d) * 1024);
+      else
+        dma16_buf(rsrcB, voffB[d - kDA], (uint32_t)(kt * BK * N + n0) * 4u,
+                  s + G::kABytes + (kDB * wave + d - kDA) * 1024);
+    } else {
+      if (d < kDA)
+        dma16(gA + (size_t)kt * BK * 4, voffA[d], s + (kDA * wave + d) * 1024);
+      else
+        dma16(gB + (size_t)kt * BK * N * 4, voffB[d - kDA], s + G::kABytes + (kDB * wave + d - kDA) * 1024);
+    }
   };
 
   const int h = lane >> 5;
@@ -524,7 +544,7 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
       for (int r = 0; r < 16; r++) {
         const int row = row0 + bi * 32 + 8 * (r >> 2) + 4 * (lane_e >> 5) + (r & 3);
         const int col = col0 + bj * 32 + (lane_e & 31);
-        C[(size_t)row * N + col] = acc[bi][bj][r];
+        if (!kEdge || (row < M && col < N)) C[(size_t)row * N + col] = acc[bi][bj][r];
       }
 #if VK_TIMELINE
   wait_vmcnt0_ordered();
@@ -540,12 +560,13 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
 #endif
 }
 
+template <bool kEdge>
 hipError_t launch_f32_mfma4(const GemmArgs& a) {
   static std::atomic<uint64_t> attr_done{0};
-  auto kfn = f32_mfma4_kernel;
+  auto kfn = f32_mfma4_kernel<kEdge>;
   hipError_t e = ensure_lds_attr(kfn, F32Cfg<32>::kLdsBytes, a.device, attr_done);
   if (e != hipSuccess) return e;
-  const int tiles = (int)((a.m / kBM) * (a.n / kBN));
+  const int tiles = kEdge ? (int)(((a.m + kBM - 1) / kBM) * ((a.n + kBN - 1) / kBN)) : (int)((a.m / kBM) * (a.n / kBN));
   hipLaunchKernelGGL(kfn, dim3(tiles), dim3(256), F32Cfg<32>::kLdsBytes, a.stream, static_cast<const float*>(a.A),
                      static_cast<const float*>(a.B), static_cast<float*>(a.C), (int)a.m, (int)a.n, (int)a.k);
   return hipGetLastError();
@@ -566,7 +587,7 @@ hipError_t launch_bk(const GemmArgs& a) {
   return hipGetLastError();
 }
 
-hipError_t launch_f32_mfma(const GemmArgs& a) { return a.k % 32 == 0 ? launch_f32_mfma4(a) : launch_bk<16>(a); }
+hipError_t launch_f32_mfma(const GemmArgs& a) { return a.k % 32 == 0 ? launch_f32_mfma4<false>(a) : launch_bk<16>(a); }
 
 // 32-bit lane offsets: the rows of A one instruction covers span less than
 // 256 * K floats beyond the k-tile base and the k-rows of B 32 * N floats;
@@ -576,9 +597,12 @@ bool f32_mfma_shape_ok(size_t m, size_t n, size_t k) {
          (m / kBM) * (n / kBN) < (1ull << 31);
 }
 
-// Version 3 (any M; N, K multiples of 4): 32-deep k-tiles, the last one
-// masked; each operand below 2^31 bytes (buffer sizes and offsets).
-hipError_t launch_f32_mfma_edge(const GemmArgs& a) { return launch_bk<32, true>(a); }
+// Version 3 (any M; N, K multiples of 4): 32-deep k-tiles (the last one
+// masked where K % 32 != 0); each operand below 2^31 bytes (buffer sizes and
+// offsets).
+hipError_t launch_f32_mfma_edge(const GemmArgs& a) {
+  return a.k % 32 == 0 ? launch_f32_mfma4<true>(a) : launch_bk<32, true>(a);
+}
 
 bool f32_mfma_edge_shape_ok(size_t m, size_t n, size_t k) {
   return m >= 1 && n >= 4 && k >= 4 && m * k * 4 < (1ull << 31) && k * n * 4 < (1ull << 31) &&
@@ -601,7 +625,7 @@ void register_f32_mfma() {
   KernelEntry e3 = e;
   e3.version = 3;
   e3.name = "f32_v3_mfma256_edge";
-  e3.caps = make_caps(3, VK_DTYPE_F32, kOutF32, 1, 4, 4, 16, kBM, kBN, 32, kThreads, F32Cfg<32>::kLdsBytes, 0, 0);
+  e3.caps = make_caps(3, VK_DTYPE_F32, kOutF32, 1, 4, 4, 16, kBM, kBN, 32, 256, F32Cfg<32>::kLdsBytes, 0, 0);
   e3.launch = launch_f32_mfma_edge;
   e3.shape_ok = f32_mfma_edge_shape_ok;
   register_kernel(e3);
