@@ -157,6 +157,8 @@ def test_pick_version_follows_shape():
     import vibekernel_amd as vk
     assert vk.pick_version(16, 8192, 8192) == 8
     assert vk.pick_version(16, 4096, 4096) == 14   # 2048 < N <= 4096: K split over the waves too
+    assert vk.pick_version(16, 4096, 14336) == 8   # up to 32 rows with K > 12288: version 8
+    assert vk.pick_version(64, 4096, 14336) == 14
     assert vk.pick_version(128, 3072, 2048) == 14
     assert vk.pick_version(128, 2048, 8192) == 14  # N <= 2048 from 65 rows
     assert vk.pick_version(64, 2048, 8192) == 8

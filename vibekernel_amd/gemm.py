@@ -143,8 +143,16 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
     against 21.7, 128 x 4096 x 14336 39.1 against 34.4), and version 8 keeps
     them.
     Version 14 (K split over the waves of a workgroup, 64-column blocks) is
-    taken up to M = 64 where 2048 < N <= 4096, and from M = 65 to 128 where
-    N <= 4096 and K <= 4096, or N <= 2048 and K <= 8192.  Measured on MI355X
+    taken up to M = 64 where 2048 < N <= 4096 (but not up to M = 32 with
+    K > 12288), and from M = 65 to 128 where N <= 4096 and K <= 4096, or
+    N <= 2048 and K <= 8192.  At K = 14336, N = 4096 version 8 is faster up
+    to M = 32 (us per launch against version 14, 2 rounds on one box: M = 1
+    22.3 against 22.6, 16 22.5 against 23.6, 32 23.8 against 24.1; N =
+    3072, M = 16 19.1 against 20.1; N = 2560, M = 16 17.8 against 18.0) and
+    version 14 from M = 48 (26.1 against 25.4; M = 64 28.4 against 27.2);
+    at K = 11264 they are within 2 % (M = 16 19.4 / 19.8, M = 1 19.1 /
+    18.9) and at K = 8192 version 14 wins (M = 1 16.4 / 15.5, 16 16.9 /
+    16.0, 32 18.4 / 16.5).  Measured on MI355X
     against version 8 (us per launch, one box, M = 1 / 16 / 64 / 128):
     N = 4096, K = 4096 8.1 / 9.1 / 14.4 / 18.4 against 9.5 / 9.9 / 16.2 /
     21.8; N = 3072, K = 2048 7.2 / 7.6 / 11.6 / 14.4 against 8.1 / 8.3 /
@@ -177,6 +185,8 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
 
     def v14_suits():
         if m > 128 or n > 4096:
+            return False
+        if m <= 32 and k > 12288:
             return False
         if m <= 64:
             return n > 2048
