@@ -12,6 +12,7 @@ pytestmark = pytest.mark.gpu
 F16_CASES = [
     ((1, 256, 64), 8),           # one row: the skinny split-K kernel
     ((16, 4096, 4096), 14),      # 2048 < N <= 4096: K split over the waves of a workgroup too
+    ((16, 4096, 14336), 8),      # up to 32 rows with K > 12288: version 8 again
     ((100, 3000, 2048), 14),     # a last column block of 56 columns
     ((128, 2048, 8192), 14),     # N <= 2048 from 65 rows
     ((160, 1024, 2048), 8),      # 2 x 2 waves
