@@ -73,7 +73,36 @@ static int check_plan(int tiles_m, int tiles_n, int I, int C, const SkPlan& p, i
   return 0;
 }
 
+// xcd_remap is a bijection of [0, total) whose image of the workgroups of
+// XCD x (bid % 8 == x) is one contiguous range, the ranges in XCD order.
+static int check_remap() {
+  for (int total = 1; total <= 4200; total++) {
+    std::vector<int> lo(8, total), hi(8, -1), cnt(8, 0), seen(total, 0);
+    for (int b = 0; b < total; b++) {
+      const int c = xcd_remap(b, total), x = b % 8;
+      if (c < 0 || c >= total || seen[c]++) {
+        std::printf("FAIL xcd_remap not a bijection: total %d\n", total);
+        return 1;
+      }
+      lo[x] = c < lo[x] ? c : lo[x];
+      hi[x] = c > hi[x] ? c : hi[x];
+      cnt[x]++;
+    }
+    int next = 0;
+    for (int x = 0; x < 8; x++) {
+      if (cnt[x] == 0) continue;
+      if (lo[x] != next || hi[x] - lo[x] + 1 != cnt[x]) {
+        std::printf("FAIL xcd_remap share of XCD %d not contiguous: total %d\n", x, total);
+        return 1;
+      }
+      next = hi[x] + 1;
+    }
+  }
+  return 0;
+}
+
 int main() {
+  if (check_remap()) return 1;
   long long cases = 0, split_plans = 0, forced = 0;
   const int Is[] = {1, 4, 8, 15, 16, 17, 31, 32, 43, 64, 65, 100, 128, 172, 256};
   const int Cs[] = {256, 240, 304, 80, 64, 8, 1};

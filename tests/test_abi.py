@@ -161,6 +161,12 @@ def test_pick_version_follows_shape():
     assert vk.pick_version(64, 4096, 14336) == 14
     assert vk.pick_version(128, 3072, 2048) == 14
     assert vk.pick_version(128, 2048, 8192) == 14  # N <= 2048 from 65 rows
+    assert vk.pick_version(96, 4096, 8192) == 14   # 65-128 rows: K up to 8192
+    assert vk.pick_version(128, 4096, 11264) == 8
+    assert vk.pick_version(1, 1536, 8192) == 14    # up to 8 rows at 1024 < N <= 2048, K <= 8192
+    assert vk.pick_version(16, 2048, 8192) == 8
+    assert vk.pick_version(1, 1024, 2048) == 8
+    assert vk.pick_version(160, 4096, 4096) == 11  # from 129 rows: 128 x 128 tiles where they suit
     assert vk.pick_version(64, 2048, 8192) == 8
     assert vk.pick_version(16, 1024, 2048) == 8
     assert vk.pick_version(1, 5120, 4096) == 8     # 80 column blocks of 64 x 2 pieces: CUs idle
@@ -168,11 +174,11 @@ def test_pick_version_follows_shape():
     assert vk.pick_version(16, 8224, 8192) == 8  # n % 128 != 0: the last column block cut short
     assert vk.pick_version(16, 8220, 8192) == 1  # n % 8 != 0: the any-shape kernel
     assert vk.pick_version(128, 8192, 8192) == 8  # batch-128 decode: still the split-K kernel
-    assert vk.pick_version(144, 8192, 8192) == 8  # 2 x 2 waves up to 256 rows
+    assert vk.pick_version(144, 8192, 8192) == 11  # from 129 rows: 128 x 128 tiles where they suit
     assert vk.pick_version(1, 8192, 8192) == 8    # one row: the same kernel, rows past M read as zeros
-    assert vk.pick_version(256, 8192, 8192) == 11  # from 192 rows: 128 x 128 tiles, K split over idle CUs
+    assert vk.pick_version(256, 8192, 8192) == 11  # 128 x 128 tiles, K split over idle CUs
     assert vk.pick_version(192, 4096, 4096) == 11
-    assert vk.pick_version(160, 4096, 4096) == 8
+    assert vk.pick_version(136, 14336, 4096) == 11
     assert vk.pick_version(192, 28672, 8192) == 8  # 448 tiles of 128 x 128 off the grid: over 1.5 waves
     assert vk.pick_version(300, 8192, 8192) == 11  # beyond 256 rows, off the grid: 192 tiles of 128 x 128
     assert vk.pick_version(4096, 4096, 4096) == 7  # 256 tiles: one full wave

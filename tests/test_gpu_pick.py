@@ -15,8 +15,11 @@ F16_CASES = [
     ((16, 4096, 14336), 8),      # up to 32 rows with K > 12288: version 8 again
     ((100, 3000, 2048), 14),     # a last column block of 56 columns
     ((128, 2048, 8192), 14),     # N <= 2048 from 65 rows
-    ((160, 1024, 2048), 8),      # 2 x 2 waves
-    ((200, 1024, 2048), 11),     # from 192 rows: 128 x 128 tiles (off the grid, K split)
+    ((160, 1024, 2048), 11),     # from 129 rows: 128 x 128 tiles (off the grid, K split)
+    ((160, 8192, 512), 11),      # from 129 rows, 128 x 128 tiles over 2 x 64 tiles
+    ((96, 4096, 8192), 14),      # 65-128 rows: K up to 8192
+    ((1, 1536, 8192), 14),       # up to 8 rows at 1024 < N <= 2048
+    ((200, 1024, 2048), 11),     # 128 x 128 tiles (off the grid, K split)
     ((16, 8224, 256), 8),        # n % 128 != 0: the last column block cut short
     ((4096, 4096, 256), 7),      # one full wave of 256 x 256 tiles
     ((512, 512, 512), 11),       # 16 tiles of 128 x 128 where 256 x 256 gives 4 (and no split)

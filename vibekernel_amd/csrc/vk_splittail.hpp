@@ -24,7 +24,8 @@
 // positions of each XCD's share (xcd_remap) and the tail is the rest of each
 // share: unit u runs on XCD u % 8 (dp is a multiple of 8) and takes the
 // pieces of that XCD's r / 8 tail tiles ("chunks" = 8); otherwise there is one
-// chunk.
+// chunk: the whole tiles are positions [0, dp), dealt to the XCDs by
+// xcd_remap over dp, and the tail the positions after them.
 #pragma once
 
 #include "vk_tile.hpp"
@@ -138,7 +139,9 @@ __host__ __device__ inline int sk_unit_of(const SkPlan& pl, int T, int tile, int
 __host__ __device__ inline SkWork sk_work(int bid, int T, int I, const SkPlan& pl, int extra = kSkLastExtra) {
   SkWork w{};
   if (bid < pl.dp) {
-    w.cid = xcd_remap(bid, T);
+    // whole tiles: raster positions [0, dp) (with 8 chunks: the first dp / 8
+    // of each XCD's share of [0, T))
+    w.cid = xcd_remap(bid, pl.chunks == 8 ? T : pl.dp);
     w.kb = 0;
     w.ke = I;
     w.np = 1;

@@ -117,8 +117,9 @@ def _num_cus() -> int:
 def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = None) -> int:
     """The fastest version that accepts this shape (checked with vk_gemm_check
     on 4 KiB-aligned placeholder addresses; nothing is launched): for fp16
-    the skinny kernels when M < 192 (version 14 where it suits, else version
-    8; version 4 up to 64), then the
+    the skinny kernels up to M = 128 (version 14 where it suits, else version
+    8; version 4 up to 64) and version 8 from 129 to 255 rows where version 11
+    does not suit, then the
     128 x 128 tiles of version 11 where they suit the grid, then the 256x256 kernels
     (fastest first; version 10 takes shapes off the 256 x 256 x 64 grid
     whose N and K are multiples of 8), then the any-shape kernel.  Version 11
@@ -135,17 +136,31 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
         slower on every such shape: 1000 x 1000 x 1000 23.0 us against 9.8,
         2000 x 3000 x 1000 (T = 384) 25.2 against 21.2, 1000 x 1000 x 4000
         (T = 64) 36.6 against 23.0).
-    From M = 192 to 256 version 11 also beats the skinny split-K version 8
-    wherever it is taken (us per launch, one box: 192 x 4096 x 4096 22.5
-    against 30.2, 192 x 8192 x 8192 39.8 against 46.0, 192 x 14336 x 4096
-    32.9 against 42.4, 256 x 8192 x 8192 39.8 against 55.6); below 192 rows
-    the two trade places with N and K (M = 128: 128 x 4096 x 4096 18.5
-    against 21.7, 128 x 4096 x 14336 39.1 against 34.4), and version 8 keeps
-    them.
+    From M = 129 version 11 also beats the skinny split-K version 8 wherever
+    it is taken (us per launch, one box: 192 x 4096 x 4096 22.5 against
+    30.2, 192 x 8192 x 8192 39.8 against 46.0, 192 x 14336 x 4096 32.9
+    against 42.4, 256 x 8192 x 8192 39.8 against 55.6; another box, v11
+    against v8 at N x K = 4096 x 4096 / 4096 x 8192 / 8192 x 4096 / 8192 x
+    8192 / 14336 x 4096 / 4096 x 14336: M = 136 21.1 / 27.1 / 24.1 / 37.1 /
+    28.9 / 37.9 against 25.9 / 31.5 / 27.0 / 37.4 / 32.8 / 39.4; M = 160
+    21.1 / 27.8 / 24.5 / 39.0 / 31.1 / 39.5 against 26.2 / 31.9 / 27.6 /
+    38.5 / 33.8 / 39.8; M = 184 21.9 / 28.3 / 24.8 / 39.8 / 32.6 / 38.9
+    against 30.3 / 38.7 / 32.5 / 45.6 / 41.1 / 46.9).
     Version 14 (K split over the waves of a workgroup, 64-column blocks) is
     taken up to M = 64 where 2048 < N <= 4096 (but not up to M = 32 with
-    K > 12288), and from M = 65 to 128 where N <= 4096 and K <= 4096, or
-    N <= 2048 and K <= 8192.  At K = 14336, N = 4096 version 8 is faster up
+    K > 12288) and up to M = 8 where 1024 < N <= 2048 and K <= 8192, and
+    from M = 65 to 128 where N <= 4096 and K <= 8192.  Against version 8
+    (us per launch, one box): M = 72 / 96 / 128 at N x K = 4096 x 6144
+    16.8 / 19.3 / 22.9 against 20.2 / 22.6 / 25.0, at 4096 x 8192 19.2 /
+    22.2 / 26.6 against 22.7 / 24.3 / 27.7, at 2048 x 8192 16.5 / 18.2 /
+    21.5 against 18.9 / 20.5 / 24.1, at 3072 x 6144 17.4 / 19.5 / 23.1
+    against 18.3 / 20.0 / 22.9; at K = 11264 mixed (4096 columns: 23.7 /
+    27.9 / 34.2 against 26.7 / 28.3 / 31.3); M = 1 / 4 / 8 at N x K = 1536 x
+    8192 8.6 / 9.0 / 9.2 against 10.0 / 10.2 / 10.3, 2048 x 8192 9.6 / 10.1
+    / 10.6 against 10.4 / 10.7 / 10.7, 2048 x 4096 8.7 / 9.0 / 9.2 against
+    8.9 / 9.1 / 9.2, but 2048 x 14336 16.0 / 16.5 / 16.4 against 15.7 /
+    15.9 / 16.0 and M = 16 at N = 2048 (K = 4096 / 8192 / 14336: 9.3 / 11.1
+    / 16.4 against 9.1 / 10.8 / 16.0).  At K = 14336, N = 4096 version 8 is faster up
     to M = 32 (us per launch against version 14, 2 rounds on one box: M = 1
     22.3 against 22.6, 16 22.5 against 23.6, 32 23.8 against 24.1; N =
     3072, M = 16 19.1 against 20.1; N = 2560, M = 16 17.8 against 18.0) and
@@ -189,15 +204,15 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
         if m <= 32 and k > 12288:
             return False
         if m <= 64:
-            return n > 2048
-        return k <= 4096 or (n <= 2048 and k <= 8192)
+            return n > 2048 or (m <= 8 and n > 1024 and k <= 8192)
+        return k <= 8192
 
     for v in order:
         if v not in avail:
             continue
         if v == 14 and not v14_suits():
             continue
-        if v == 8 and m >= 192 and in_dt == DTYPE_F16 and v11_suits() and takes(11):
+        if v == 8 and m > 128 and in_dt == DTYPE_F16 and v11_suits() and takes(11):
             continue
         if v == 9 and _abi.workspace_bytes(v, in_dt, m, n, k) == 0:
             continue
