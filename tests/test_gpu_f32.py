@@ -4,10 +4,13 @@
 * version 1 (VALU, one fmaf per term in ascending k): equal to the oracle,
   bit for bit, on every shape;
 * version 2 (matrix cores, v_mfma_f32_32x32x2_f32, two products per step;
-  the four-wave kernel when K % 32 == 0, the eight-wave one with 16-deep
-  k-tiles otherwise): integer inputs exact; random inputs within 2 k u
-  |A||B| of the exact (fp64) product; bitwise repeatable launch to launch;
-  shapes include one k-tile (K = 32) and more tiles than CUs;
+  the four-wave kernel when K % 32 == 0 -- 256 x 256 tiles where they give
+  every CU one, else 128 x 128 tiles, K split over idle CUs where those fill
+  at most half of them -- the eight-wave one with 16-deep k-tiles
+  otherwise): integer inputs exact; random inputs within 2 k u |A||B| of
+  the exact (fp64) product; bitwise repeatable launch to launch (a split
+  shape); shapes include one k-tile (K = 32), more tiles than CUs, 128 x 128
+  tiles whole and split into 2 to 8 pieces;
 * version 3 (version 2 with masked edges: any M, N and K multiples of 4; the
   four-wave kernel when K % 32 == 0): the same bars on ragged shapes,
   bitwise equal to version 2 on its grid, nothing written outside C, and the
@@ -22,10 +25,16 @@ pytestmark = pytest.mark.gpu
 
 SHAPES_V1 = [(128, 128, 16), (256, 384, 64), (512, 512, 512), (1, 1, 1), (17, 33, 65), (130, 250, 70),
              (128, 256, 16), (256, 512, 32), (384, 768, 48), (1024, 512, 1024), (128, 256, 2000)]
+# (version 2, 256 CUs) 256 x 256 tiles: (4352, 4096, 64); 128 x 128 whole:
+# (512, 256, 64), (256, 256, 32), (2048, 2048, 128); split: (768, 512, 256)
+# in 2 pieces, (1024, 1024, 512), (512, 512, 512) and (1024, 1024, 1024) in
+# 4, (256, 256, 1024) in 8
 SHAPES_V2 = [(256, 256, 16), (512, 256, 64), (256, 512, 48), (768, 512, 256), (1024, 1024, 512), (256, 256, 32),
-             (4352, 4096, 64)]
+             (4352, 4096, 64), (512, 512, 512), (1024, 1024, 1024), (256, 256, 1024), (2048, 2048, 128)]
+# split edge tiles: (1000, 1000, 1024) 4 pieces, (300, 600, 2048) and
+# (129, 4, 512) 8 and 4
 SHAPES_V3 = [(1, 4, 4), (17, 36, 68), (300, 260, 100), (257, 512, 36), (1000, 1000, 1000), (256, 256, 64),
-             (300, 260, 96), (257, 516, 64), (1000, 1000, 1024), (1, 4, 32)]
+             (300, 260, 96), (257, 516, 64), (1000, 1000, 1024), (1, 4, 32), (300, 600, 2048), (129, 4, 512)]
 CASES = [(1, s) for s in SHAPES_V1] + [(2, s) for s in SHAPES_V2] + [(3, s) for s in SHAPES_V3]
 
 
@@ -87,7 +96,9 @@ def test_f32_4096(gpu, oracle, version):
 
 
 def test_f32_mfma_repeat_deterministic(gpu):
-    """20 launches of version 2 with C poisoned before each: bitwise equal."""
+    """20 launches of version 2 with C poisoned before each: bitwise equal
+    (48 tiles of 128 x 128, K split in 4: whichever piece arrives last, the
+    pieces are summed in k order)."""
     import torch
     import vibekernel_amd as vk
     m, n, k = 1024, 768, 512
@@ -118,8 +129,8 @@ def test_f32_mfma_rejects_unaligned_shape(gpu):
 
 def test_f32_edge_on_grid_equals_v2(gpu):
     """On version 2's grid with K % 32 == 0 both run 32-deep k-tiles in the
-    same order: bitwise equal."""
-    for m, n, k in [(256, 256, 64), (512, 768, 320), (256, 512, 32)]:
+    same order, with the same tiles and split: bitwise equal."""
+    for m, n, k in [(256, 256, 64), (512, 768, 320), (256, 512, 32), (512, 512, 512), (256, 256, 1024)]:
         A, B = make_inputs(m, n, k, "normal", seed=m + k, dtype=np.float32)
         assert np.array_equal(_run(A, B, 2).view(np.uint32), _run(A, B, 3).view(np.uint32))
 

@@ -44,6 +44,7 @@
 // equality.
 #include "vk_device.hpp"
 #include "vk_internal.hpp"
+#include "vk_splittail.hpp"
 #include "vk_tile.hpp"
 
 #include <atomic>
@@ -305,64 +306,225 @@ extern "C" int vk_timeline_f32_read(unsigned long long* host, int waves) {
 }
 #endif
 
-// Four-wave kernel (versions 2 and 3, K % 32 == 0): the eight-wave kernel's tile,
-// 32-deep k-tiles, LDS layout, loads and per-element k order, with one wave
-// per SIMD owning a 128x128 quarter (4x4 blocks of 32x32: 256 fp32
-// accumulators per lane in AGPRs); wave w owns rows 128*(w/2) and columns
-// 128*(w%2) onward.  Per k-tile a wave reads 16 KB of A and 16 KB of B
-// fragments (the eight-wave kernel's waves 16 + 8 KB each, two per SIMD):
-// a third less LDS data per MFMA.  Its fragments are read one group of 4
-// steps ahead into a second register set, one read after each of the first
-// 12 MFMAs of the group's second step; the k-tile's one barrier sits after
-// the first step of its last group (whose fragments are already in
-// registers), followed by the next k-tile's first group of reads and, one
-// after every third MFMA of the last three steps, the 16 loads that refill
-// the slot just freed with k-tile t + 2 (clamped to the last k-tile: a
-// refill past the end rewrites the last k-tile's data into a slot nobody
-// reads).  Measured per k-tile (timeline build, 4096^3): 17,113 shader
-// cycles against the 16,384 its MFMAs need on every XCD (0.957); instrumented
-// copies without the fragment reads took 16,420 (the A reads' 16
-// ds_read_b128 cost ~510 cycles, the B reads' 32 ds_read2st64_b32 ~225),
-// without the loads 16,988, without the barrier 17,090.
-template <bool kEdge>
+// Four-wave kernel (versions 2 and 3, K % 32 == 0): the eight-wave kernel's
+// 32-deep k-tiles, LDS layout, loads and per-element k order on tiles of
+// 64 kNB x 64 kNB, one wave per SIMD owning a quarter of 32 kNB x 32 kNB
+// (kNB x kNB blocks of 32x32); wave w owns rows 32 kNB (w / 2) and columns
+// 32 kNB (w % 2) onward.
+//  * kNB = 4, 256x256 tiles (256 fp32 accumulators per lane in AGPRs), where
+//    those tiles give every CU one: per k-tile a wave reads 16 KB of A and
+//    16 KB of B fragments (the eight-wave kernel's waves 16 + 8 KB each, two
+//    per SIMD), a third less LDS data per MFMA.  Measured per k-tile
+//    (timeline build, 4096^3): 17,113 shader cycles against the 16,384 its
+//    MFMAs need on every XCD (0.957); instrumented copies without the
+//    fragment reads took 16,420 (the A reads' 16 ds_read_b128 cost ~510
+//    cycles, the B reads' 32 ds_read2st64_b32 ~225), without the loads
+//    16,988, without the barrier 17,090.
+//  * kNB = 2, 128x128 tiles (64 accumulators per lane), for grids whose
+//    256x256 tiles would leave CUs idle (1024^3: 16 of them on 256 CUs):
+//    four times as many tiles, and where even those fill at most half of
+//    the CUs, K is split over the idle ones (kSplit, below).  An fp32 MFMA
+//    takes 64 cycles, so a wave's 128x128x32 k-tile is 4096 cycles of MFMA
+//    against 16 KB of fragment reads and 8 KB of loads: the smaller tile
+//    costs the matrix cores nothing.
+// A wave's fragments are read one group of 4 steps ahead into a second
+// register set: the next group's kReads reads (kNB A reads of 16 bytes, 2 kNB
+// pairs of B values) one after each of the first kReads MFMAs from the
+// group's second step on.  The k-tile's one barrier sits after the first
+// step of its last group (whose fragments are already in registers),
+// followed by the next k-tile's first group of reads and, one after every
+// kLoadEvery-th MFMA of the last three steps, the kD loads that refill the
+// slot just freed with k-tile t + 2 (clamped to the last k-tile: a refill
+// past the end rewrites the last k-tile's data into a slot nobody reads).
+template <int kNB>
+struct F32W4 {
+  static constexpr int BK = 32;
+  static constexpr int kT = 64 * kNB;                    // tile side
+  static constexpr int kQ = 32 * kNB;                    // a wave's quarter
+  static constexpr int kABytes = kT * BK * 4;            // kT rows of 128 B
+  static constexpr int kBRow = kT * 4;                   // bytes of a B k-row
+  static constexpr int kStageBytes = kABytes + BK * kBRow;
+  static constexpr int kLdsBytes = 2 * kStageBytes;      // 128 or 64 KB
+  static constexpr int kRowChunks = BK / 4;              // 16-byte chunks per A row
+  static constexpr int kSteps = BK / 2;                  // MFMA k-steps per k-tile
+  static constexpr int kDA = kT / 32;                    // A loads per wave per k-tile (8 rows each)
+  static constexpr int kBRowsPerDma = 1024 / kBRow;      // B k-rows per 1 KB load
+  static constexpr int kDB = BK / kBRowsPerDma / 4;      // B loads per wave per k-tile
+  static constexpr int kD = kDA + kDB;
+  static constexpr int kReads = 3 * kNB;                 // fragment reads per group of 4 steps
+  static constexpr int kLoadEvery = 3 * kNB * kNB / kD;  // MFMAs per load in the last 3 steps
+  static_assert(kLdsBytes <= 160 * 1024 && kLoadEvery >= 1 && kD * kLoadEvery <= 3 * kNB * kNB, "schedule");
+  static_assert(kReads <= 3 * kNB * kNB, "a group's reads fit its last three steps");
+};
+
+// ---- split K (kNB = 2) for grids whose 128x128 tiles fill at most half of
+// the CUs: sk_plan_fill's pieces (at least kF32MinIters k-tiles each, the
+// last one k-tile longer), the pieces of a tile meeting as in the fp16
+// 128x128 kernel: per (tile, wave) an arrival counter; a finishing wave that
+// finds every other piece in memory is the last and writes nothing,
+// otherwise it writes its 16 KB fp32 partial with sc1 stores, waits for them
+// and increments the counter, and the one that sees np - 1 is the last.  The
+// last sums P0 + P1 + ... in k order (its own piece from registers), so C
+// does not depend on the arrival order, stores C and resets the counter.
+// A piece of 4 k-tiles is ~8 us of MFMA at the board's clock, twice the
+// hand-off (its partial published, then read back by the last arrival).
+constexpr int kF32MinIters = 4;
+constexpr size_t kF32SlotBytes = (size_t)128 * 128 * sizeof(float);  // one tile's fp32 partial
+constexpr uint32_t kF32WaveBytes = 64 * 64 * sizeof(float);          // a wave's 64x64 quarter
+
+__host__ __device__ inline int64_t f32_tiles(size_t m, size_t n, size_t t) {
+  return (int64_t)((m + t - 1) / t) * (int64_t)((n + t - 1) / t);
+}
+// 128x128 tiles where the 256x256 ones leave CUs without a tile.
+inline bool f32_small_tiles(size_t m, size_t n, int num_cus) { return f32_tiles(m, n, 256) < num_cus; }
+inline SkPlan f32_plan(size_t m, size_t n, size_t k, int num_cus) {
+  return sk_plan_fill(f32_tiles(m, n, 128), (int64_t)(k / 32), num_cus, kF32MinIters);
+}
+
+// Vector v of a wave's accumulators: block (v / 4kNB, (v / 4) % kNB),
+// registers 4 (v % 4) .. + 3.  In a partial, vector v of every lane sits at
+// v * 1024 + lane * 16 of the wave's region: each store a coalesced 1 KB.
+template <int kNB>
+__device__ __forceinline__ float4v acc_vec(const float16v_ (&acc)[kNB][kNB], int v) {
+  const float16v_& x = acc[v / (4 * kNB)][(v / 4) % kNB];
+  const int r = 4 * (v % 4);
+  return float4v{x[r], x[r + 1], x[r + 2], x[r + 3]};
+}
+
+// This wave holds piece p of np of its quarter; part_off(q): byte offset of
+// the wave's region of piece q's slot.  Returns whether this wave arrived
+// last.  Only the last piece, which usually arrives last, reads the counter
+// first; the others publish their partial at once.
+template <int kNB, typename PartOff>
+__device__ __forceinline__ bool f32_split_arrive(const float16v_ (&acc)[kNB][kNB], int np, int p, int lane,
+                                                 __amdgpu_buffer_rsrc_t part, PartOff part_off, unsigned* cnt) {
+  if (p == np - 1) {
+    const unsigned seen =
+        __builtin_amdgcn_readfirstlane(__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+    if (seen == (unsigned)(np - 1)) return true;  // every other piece is in memory
+  }
+  const uint32_t soff = part_off(p);
+#pragma unroll
+  for (int v = 0; v < 4 * kNB * kNB; v++) store_partial(part, (uint32_t)lane * 16 + v * 1024, soff, acc_vec(acc, v));
+  wait_vmcnt0_ordered();  // the partial is in memory before the counter moves
+  unsigned old = 0;
+  if (lane == 0) old = __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return __builtin_amdgcn_readfirstlane(old) == (unsigned)(np - 1);
+}
+
+// The last arrival: acc <- P0 + P1 + ... + P(NP-1), left to right, with
+// P(p) = acc.  Every piece's vectors are loaded kB at a time (NP x kB loads
+// in flight, at most 128 registers), the own piece's slot too (not used; it
+// always lies inside the workspace, so no branch is needed).
+template <int kNB, int NP, typename PartOff>
+__device__ __forceinline__ void f32_split_sum_n(float16v_ (&acc)[kNB][kNB], int p, int lane,
+                                                __amdgpu_buffer_rsrc_t part, PartOff part_off) {
+  constexpr int kV = 4 * kNB * kNB;
+  constexpr int kB = NP <= 4 ? 8 : 4;
+  static_assert(kV % kB == 0, "whole batches");
+#pragma unroll
+  for (int v0 = 0; v0 < kV; v0 += kB) {
+    float4v x[NP][kB];
+#pragma unroll
+    for (int q = 0; q < NP; q++) {
+      const uint32_t soff = part_off(q);
+#pragma unroll
+      for (int b = 0; b < kB; b++) x[q][b] = load_partial(part, (uint32_t)lane * 16 + (v0 + b) * 1024, soff);
+    }
+#pragma unroll
+    for (int b = 0; b < kB; b++) {
+      const int v = v0 + b;
+      const uint4v own = __builtin_bit_cast(uint4v, acc_vec(acc, v));
+      float4v t;
+#pragma unroll
+      for (int q = 0; q < NP; q++) {
+        // piece q's term: the own registers where q == p, picked by a mask
+        // the compiler cannot see through (no branch in the sum)
+        uint32_t mine = q == p ? ~0u : 0u;
+        asm volatile("" : "+v"(mine));
+        const float4v term =
+            __builtin_bit_cast(float4v, (__builtin_bit_cast(uint4v, x[q][b]) & ~mine) | (own & mine));
+        t = q == 0 ? term : t + term;
+      }
+      float16v_& dst = acc[v / (4 * kNB)][(v / 4) % kNB];
+      const int r = 4 * (v % 4);
+#pragma unroll
+      for (int e = 0; e < 4; e++) dst[r + e] = t[e];
+    }
+  }
+}
+
+template <int kNB, typename PartOff>
+__device__ __forceinline__ void f32_split_sum(float16v_ (&acc)[kNB][kNB], int np, int p, int lane,
+                                              __amdgpu_buffer_rsrc_t part, PartOff part_off) {
+  // The counter read that made this wave the last stays before these reads.
+  asm volatile("" ::: "memory");
+  static_assert(kFillMaxPieces == 8, "one case per piece count");
+  switch (np) {
+    case 2: f32_split_sum_n<kNB, 2>(acc, p, lane, part, part_off); break;
+    case 3: f32_split_sum_n<kNB, 3>(acc, p, lane, part, part_off); break;
+    case 4: f32_split_sum_n<kNB, 4>(acc, p, lane, part, part_off); break;
+    case 5: f32_split_sum_n<kNB, 5>(acc, p, lane, part, part_off); break;
+    case 6: f32_split_sum_n<kNB, 6>(acc, p, lane, part, part_off); break;
+    case 7: f32_split_sum_n<kNB, 7>(acc, p, lane, part, part_off); break;
+    default: f32_split_sum_n<kNB, 8>(acc, p, lane, part, part_off); break;
+  }
+}
+
+// kSplit: this workgroup is unit blockIdx.x of the split plan {0, units,
+// pieces, chunks}; part and counters are the workspace.
+template <int kNB, bool kEdge, bool kSplit>
 __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict__ A, const float* __restrict__ B,
-                                                        float* __restrict__ C, int M, int N, int K) {
-  constexpr int BK = 32;
-  using G = F32Cfg<BK>;
-  constexpr int kDA = 2 * G::kDmaA, kDB = 2 * G::kDmaB, kD = kDA + kDB;  // 8 + 8 loads per wave per k-tile
-  static_assert(kD == 16, "one load per MFMA of a step");
+                                                        float* __restrict__ C, int M, int N, int K, int units,
+                                                        int pieces, int chunks, float* __restrict__ part,
+                                                        unsigned* __restrict__ counters) {
+  using W = F32W4<kNB>;
+  constexpr int BK = W::BK, kT = W::kT, kQ = W::kQ;
+  constexpr int kDA = W::kDA, kDB = W::kDB, kD = W::kD;
+  static_assert(!kSplit || kNB == 2, "K is split on the 128x128 tiles only");
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wr = wave >> 1, wc = wave & 1;
-  int tm, tn;
-  tile_of(blockIdx.x, (M + (kEdge ? kBM - 1 : 0)) / kBM, (N + (kEdge ? kBN - 1 : 0)) / kBN, tm, tn);
-  const int m0 = tm * kBM, n0 = tn * kBN;
+  const int tiles_m = (M + (kEdge ? kT - 1 : 0)) / kT, tiles_n = (N + (kEdge ? kT - 1 : 0)) / kT;
+  const int iters = K / BK;
+  int tm, tn, kb = 0, nk = iters;
+  SkWork w{};
+  if constexpr (kSplit) {
+    w = sk_work(blockIdx.x, tiles_m * tiles_n, iters, SkPlan{0, units, pieces, chunks}, kFillLastExtra);
+    raster_tile(w.cid, tiles_m, tiles_n, tm, tn);
+    kb = w.kb;
+    nk = w.ke - w.kb;
+  } else {
+    tile_of(blockIdx.x, tiles_m, tiles_n, tm, tn);
+  }
+  const int m0 = tm * kT, n0 = tn * kT;
   const uint32_t lds_base = lds_addr32(lds);
 
 #if VK_TIMELINE
   const unsigned long long tl_entry = __builtin_amdgcn_s_memrealtime();
   unsigned long long tl_bar = 0;
 #endif
-  // Load d < 8 of a wave is A instruction 8 w + d (8 rows of 128 bytes),
-  // load 8 + e its B instruction 8 w + e (the k-row of that number, 1 KB).
+  // Load d < kDA of a wave is A instruction kDA w + d (8 rows of 128 bytes),
+  // load kDA + e its B instruction kDB w + e (kBRowsPerDma k-rows, 1 KB).
   constexpr int kRowsPerDma = 1024 / (4 * BK);
+  constexpr int kBLanesPerRow = 64 / W::kBRowsPerDma;
   uint32_t voffA[kDA], voffB[kDB];
 #pragma unroll
   for (int d = 0; d < kDA; d++) {
     const int i = kDA * wave + d;
-    const int row = kRowsPerDma * i + lane / G::kRowChunks;
-    const int ca = (lane % G::kRowChunks) ^ swz_a32<BK>(row);
+    const int row = kRowsPerDma * i + lane / W::kRowChunks;
+    const int ca = (lane % W::kRowChunks) ^ swz_a32<BK>(row);
     voffA[d] = (uint32_t)(((size_t)row * K + ca * 4) * 4);
   }
 #pragma unroll
   for (int d = 0; d < kDB; d++) {
-    const int i = kDB * wave + d;
-    const int cb = lane ^ swz_b32<BK>(i);
-    voffB[d] = (uint32_t)(((size_t)i * N + cb * 4) * 4);
+    const int krow = W::kBRowsPerDma * (kDB * wave + d) + lane / kBLanesPerRow;
+    const int cb = (lane % kBLanesPerRow) ^ swz_b32<BK>(krow);
+    voffB[d] = (uint32_t)(((size_t)krow * N + cb * 4) * 4);
   }
-  const char* gA = reinterpret_cast<const char*>(A) + (size_t)m0 * K * 4;
-  const char* gB = reinterpret_cast<const char*>(B) + (size_t)n0 * 4;
+  const char* gA = reinterpret_cast<const char*>(A) + ((size_t)m0 * K + (size_t)kb * BK) * 4;
+  const char* gB = reinterpret_cast<const char*>(B) + ((size_t)kb * BK * N + n0) * 4;
   const uint32_t sizeA = kEdge ? (uint32_t)M * (uint32_t)K * 4u : 0u;
   const uint32_t sizeB = kEdge ? (uint32_t)K * (uint32_t)N * 4u : 0u;
   const __amdgpu_buffer_rsrc_t rsrcA =
@@ -370,88 +532,88 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
   const __amdgpu_buffer_rsrc_t rsrcB =
       __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(B), 0, (int)sizeB, kBufferWord3);
   auto issue_one = [&](int kt, int slot, int d) {
-    const uint32_t s = lds_base + slot * G::kStageBytes;
+    const uint32_t s = lds_base + slot * W::kStageBytes;
     if constexpr (kEdge) {
       // K % 32 == 0: only rows past M and columns past N; the buffer ranges
       // give zeros past each matrix (B columns past N read the next row's,
       // feeding only C columns that are not stored)
       if (d < kDA)
-        dma16_buf(rsrcA, voffA[d], (uint32_t)(m0 * K + kt * BK) * 4u, s + (kDA * wave + d) * 1024);
+        dma16_buf(rsrcA, voffA[d], (uint32_t)(m0 * K + (kb + kt) * BK) * 4u, s + (kDA * wave + d) * 1024);
       else
-        dma16_buf(rsrcB, voffB[d - kDA], (uint32_t)(kt * BK * N + n0) * 4u,
-                  s + G::kABytes + (kDB * wave + d - kDA) * 1024);
+        dma16_buf(rsrcB, voffB[d - kDA], (uint32_t)((kb + kt) * BK * N + n0) * 4u,
+                  s + W::kABytes + (kDB * wave + d - kDA) * 1024);
     } else {
       if (d < kDA)
         dma16(gA + (size_t)kt * BK * 4, voffA[d], s + (kDA * wave + d) * 1024);
       else
-        dma16(gB + (size_t)kt * BK * N * 4, voffB[d - kDA], s + G::kABytes + (kDB * wave + d - kDA) * 1024);
+        dma16(gB + (size_t)kt * BK * N * 4, voffB[d - kDA], s + W::kABytes + (kDB * wave + d - kDA) * 1024);
     }
   };
 
   const int h = lane >> 5;
-  uint32_t aoff[4][4];
+  uint32_t aoff[kNB][4];
 #pragma unroll
-  for (int bi = 0; bi < 4; bi++) {
-    const int row = wr * 128 + bi * 32 + (lane & 31);
+  for (int bi = 0; bi < kNB; bi++) {
+    const int row = wr * kQ + bi * 32 + (lane & 31);
 #pragma unroll
     for (int c = 0; c < 4; c++) aoff[bi][c] = row * (4 * BK) + 16 * ((4 * h + c) ^ swz_a32<BK>(row));
   }
-  uint32_t boff[4];
+  uint32_t boff[kNB];
 #pragma unroll
-  for (int bj = 0; bj < 4; bj++) {
-    const int col = wc * 128 + bj * 32 + (lane & 31);
-    boff[bj] = G::kABytes + G::kSteps * h * 1024 + 16 * ((col >> 2) ^ (h << 3)) + 4 * (col & 3);
+  for (int bj = 0; bj < kNB; bj++) {
+    const int col = wc * kQ + bj * 32 + (lane & 31);
+    boff[bj] = W::kABytes + W::kSteps * h * W::kBRow + 16 * ((col >> 2) ^ (h << 3)) + 4 * (col & 3);
   }
 
-  float16v_ acc[4][4];
+  float16v_ acc[kNB][kNB];
 #pragma unroll
-  for (int bi = 0; bi < 4; bi++)
+  for (int bi = 0; bi < kNB; bi++)
 #pragma unroll
-    for (int bj = 0; bj < 4; bj++)
+    for (int bj = 0; bj < kNB; bj++)
 #pragma unroll
       for (int r = 0; r < 16; r++) acc[bi][bj][r] = 0.0f;
   prefer_agpr_accumulators();
 
   struct Frag {
-    float a[4][4];  // [block][step of the group]
-    float b[4][4];
+    float a[kNB][4];  // [block][step of the group]
+    float b[kNB][4];
   };
   Frag f[2];
   auto read_group = [&](Frag& fr, uint32_t s, auto gc) {
     constexpr int g = decltype(gc)::value;
 #pragma unroll
-    for (int bi = 0; bi < 4; bi++) {
+    for (int bi = 0; bi < kNB; bi++) {
       const float4v v = lds_read_f4(s + aoff[bi][g]);
 #pragma unroll
       for (int q = 0; q < 4; q++) fr.a[bi][q] = v[q];
     }
 #pragma unroll
-    for (int bj = 0; bj < 4; bj++)
+    for (int bj = 0; bj < kNB; bj++)
 #pragma unroll
-      for (int q = 0; q < 4; q++) fr.b[bj][q] = lds_read_f32(s + boff[bj] + (4 * g + q) * 1024);
+      for (int q = 0; q < 4; q++) fr.b[bj][q] = lds_read_f32(s + boff[bj] + (4 * g + q) * W::kBRow);
   };
-  // Read i of a group (0..11): the 16-byte A read of block i (i < 4), else
-  // the two B values of block (i - 4) / 2, steps 2 ((i - 4) % 2) and + 1.
+  // Read i of a group (0 .. kReads - 1): the 16-byte A read of block i
+  // (i < kNB), else the two B values of block (i - kNB) / 2, steps
+  // 2 ((i - kNB) % 2) and + 1.
   auto read_one = [&](Frag& fr, uint32_t s, int g, int i) {
-    if (i < 4) {
+    if (i < kNB) {
       const float4v v = lds_read_f4(s + aoff[i][g]);
 #pragma unroll
       for (int q = 0; q < 4; q++) fr.a[i][q] = v[q];
     } else {
-      const int bj = (i - 4) >> 1, q = 2 * ((i - 4) & 1);
-      fr.b[bj][q] = lds_read_f32(s + boff[bj] + (4 * g + q) * 1024);
-      fr.b[bj][q + 1] = lds_read_f32(s + boff[bj] + (4 * g + q + 1) * 1024);
+      const int bj = (i - kNB) >> 1, q = 2 * ((i - kNB) & 1);
+      fr.b[bj][q] = lds_read_f32(s + boff[bj] + (4 * g + q) * W::kBRow);
+      fr.b[bj][q + 1] = lds_read_f32(s + boff[bj] + (4 * g + q + 1) * W::kBRow);
     }
   };
   auto mfma_step = [&](const Frag& fr, int q) {
 #pragma unroll
-    for (int bi = 0; bi < 4; bi++)
+    for (int bi = 0; bi < kNB; bi++)
 #pragma unroll
-      for (int bj = 0; bj < 4; bj++)
+      for (int bj = 0; bj < kNB; bj++)
         acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(fr.a[bi][q], fr.b[bj][q], acc[bi][bj], 0, 0, 0);
   };
 
-  const int nk = K / BK;
   // Prologue: k-tiles 0 and 1 (clamped) in flight, k-tile 0 waited for.
 #pragma unroll
   for (int d = 0; d < kD; d++) issue_one(0, 0, d);
@@ -466,7 +628,7 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
 #endif
 
   for (int t = 0; t < nk; t++) {
-    const uint32_t s = lds_base + (t & 1) * G::kStageBytes;
+    const uint32_t s = lds_base + (t & 1) * W::kStageBytes;
     static_for<4>([&](auto gc) {
       constexpr int g = decltype(gc)::value;
 #if VK_TIMELINE
@@ -477,19 +639,29 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
       mfma_step(f[g & 1], 0);
       __builtin_amdgcn_sched_barrier(0);
       if constexpr (g < 3) {
-        // step 1, the next group's 12 reads one after each of its first MFMAs
+        // steps 1..3, the next group's reads one after each of the first
+        // kReads MFMAs
+        static_for<3>([&](auto qc) {
+          constexpr int q = decltype(qc)::value + 1;
+          if constexpr ((q - 1) * kNB * kNB < W::kReads) {
 #pragma unroll
-        for (int bi = 0; bi < 4; bi++)
+            for (int bi = 0; bi < kNB; bi++)
 #pragma unroll
-          for (int bj = 0; bj < 4; bj++) {
-            const int m = 4 * bi + bj;
-            acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(f[g & 1].a[bi][1], f[g & 1].b[bj][1], acc[bi][bj], 0, 0, 0);
-            if (m < 12) {
-              __builtin_amdgcn_sched_barrier(0);
-              read_one(f[(g + 1) & 1], s, g + 1, m);
-            }
+              for (int bj = 0; bj < kNB; bj++) {
+                const int m = (q - 1) * kNB * kNB + kNB * bi + bj;
+                acc[bi][bj] =
+                    __builtin_amdgcn_mfma_f32_32x32x2f32(f[g & 1].a[bi][q], f[g & 1].b[bj][q], acc[bi][bj], 0, 0, 0);
+                if (m < W::kReads) {
+                  __builtin_amdgcn_sched_barrier(0);
+                  read_one(f[(g + 1) & 1], s, g + 1, m);
+                }
+                __builtin_amdgcn_sched_barrier(0);
+              }
+          } else {
             __builtin_amdgcn_sched_barrier(0);
+            mfma_step(f[g & 1], q);
           }
+        });
       } else {
         wait_lgkmcnt0();
         wait_vmcnt<0>();  // this wave's loads of k-tile t + 1
@@ -497,34 +669,29 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
 #if VK_TIMELINE
         tl_bar += __builtin_amdgcn_s_memtime() - tl_b0;
 #endif
-        const uint32_t s_next = lds_base + ((t + 1) & 1) * G::kStageBytes;
+        const uint32_t s_next = lds_base + ((t + 1) & 1) * W::kStageBytes;
         const int kt_next = min(t + 2, nk - 1);
-        // steps 1..3 (48 MFMAs): the next k-tile's first 12 reads after the
-        // first 12, a load after every third, A and B alternating
+        // steps 1..3: the next k-tile's first kReads reads after the first
+        // kReads MFMAs, a load after every kLoadEvery-th, A and B alternating
 #pragma unroll
         for (int q = 1; q < 4; q++)
 #pragma unroll
-          for (int bi = 0; bi < 4; bi++)
+          for (int bi = 0; bi < kNB; bi++)
 #pragma unroll
-            for (int bj = 0; bj < 4; bj++) {
-              const int m = 16 * (q - 1) + 4 * bi + bj;
+            for (int bj = 0; bj < kNB; bj++) {
+              const int m = kNB * kNB * (q - 1) + kNB * bi + bj;
               __builtin_amdgcn_sched_barrier(0);
               acc[bi][bj] = __builtin_amdgcn_mfma_f32_32x32x2f32(f[1].a[bi][q], f[1].b[bj][q], acc[bi][bj], 0, 0, 0);
-              if (m < 12) {
+              if (m < W::kReads) {
                 __builtin_amdgcn_sched_barrier(0);
                 read_one(f[0], s_next, 0, m);
               }
-              if (m % 3 == 0 && m / 3 < kD) {
-                const int d = m / 3;
+              if (m % W::kLoadEvery == 0 && m / W::kLoadEvery < kD) {
+                const int d = m / W::kLoadEvery;
                 __builtin_amdgcn_sched_barrier(0);
                 issue_one(kt_next, t & 1, (d & 1) ? kDA + (d >> 1) : (d >> 1));
               }
             }
-      }
-      if constexpr (g < 3) {
-        __builtin_amdgcn_sched_barrier(0);
-        mfma_step(f[g & 1], 2);
-        mfma_step(f[g & 1], 3);
       }
     });
   }
@@ -535,17 +702,33 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
 #endif
 
   const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
-  const int row0 = m0 + wr * 128, col0 = n0 + wc * 128;
+  unsigned* cnt = nullptr;
+  if constexpr (kSplit) {
+    const __amdgpu_buffer_rsrc_t prsrc =
+        __builtin_amdgcn_make_buffer_rsrc(part, 0, (int)((size_t)units * kF32SlotBytes), kBufferWord3);
+    const SkPlan plan{0, units, pieces, chunks};
+    const int T = tiles_m * tiles_n;
+    auto part_off = [&](int q) {
+      return (uint32_t)((size_t)sk_unit_of(plan, T, w.tile, q) * kF32SlotBytes) + (uint32_t)wave * kF32WaveBytes;
+    };
+    cnt = counters + (size_t)w.tile * kSkWaves + wave;
+    if (!f32_split_arrive(acc, w.np, w.p, lane_e, prsrc, part_off, cnt)) return;
+    f32_split_sum(acc, w.np, w.p, lane_e, prsrc, part_off);
+  }
+  const int row0 = m0 + wr * kQ, col0 = n0 + wc * kQ;
 #pragma unroll
-  for (int bi = 0; bi < 4; bi++)
+  for (int bi = 0; bi < kNB; bi++)
 #pragma unroll
-    for (int bj = 0; bj < 4; bj++)
+    for (int bj = 0; bj < kNB; bj++)
 #pragma unroll
       for (int r = 0; r < 16; r++) {
         const int row = row0 + bi * 32 + 8 * (r >> 2) + 4 * (lane_e >> 5) + (r & 3);
         const int col = col0 + bj * 32 + (lane_e & 31);
         if (!kEdge || (row < M && col < N)) C[(size_t)row * N + col] = acc[bi][bj][r];
       }
+  if constexpr (kSplit) {
+    if (lane_e == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
 #if VK_TIMELINE
   wait_vmcnt0_ordered();
   const unsigned long long tl_exit = __builtin_amdgcn_s_memrealtime();
@@ -560,16 +743,44 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
 #endif
 }
 
+template <int kNB, bool kEdge, bool kSplit>
+hipError_t launch_w4(const GemmArgs& a, const SkPlan& p) {
+  using W = F32W4<kNB>;
+  static std::atomic<uint64_t> attr_done{0};
+  auto kfn = f32_mfma4_kernel<kNB, kEdge, kSplit>;
+  hipError_t e = ensure_lds_attr(kfn, W::kLdsBytes, a.device, attr_done);
+  if (e != hipSuccess) return e;
+  unsigned* counters = nullptr;
+  float* part = nullptr;
+  if constexpr (kSplit) {
+    counters = static_cast<unsigned*>(a.workspace);
+    part = reinterpret_cast<float*>(static_cast<char*>(a.workspace) + kSkCounterBytes);
+    if (!a.workspace_clean) {
+      e = zero_words(counters, kSkCounterBytes / sizeof(unsigned), a.stream);
+      if (e != hipSuccess) return e;
+    }
+  }
+  const int grid = kSplit ? p.units : (int)f32_tiles(a.m, a.n, W::kT);
+  hipLaunchKernelGGL(kfn, dim3(grid), dim3(256), W::kLdsBytes, a.stream, static_cast<const float*>(a.A),
+                     static_cast<const float*>(a.B), static_cast<float*>(a.C), (int)a.m, (int)a.n, (int)a.k, p.units,
+                     p.pieces, p.chunks, part, counters);
+  return hipGetLastError();
+}
+
+// 256x256 tiles where they give every CU one; otherwise 128x128 tiles, with
+// K split where those fill at most half of the CUs.
 template <bool kEdge>
 hipError_t launch_f32_mfma4(const GemmArgs& a) {
-  static std::atomic<uint64_t> attr_done{0};
-  auto kfn = f32_mfma4_kernel<kEdge>;
-  hipError_t e = ensure_lds_attr(kfn, F32Cfg<32>::kLdsBytes, a.device, attr_done);
-  if (e != hipSuccess) return e;
-  const int tiles = kEdge ? (int)(((a.m + kBM - 1) / kBM) * ((a.n + kBN - 1) / kBN)) : (int)((a.m / kBM) * (a.n / kBN));
-  hipLaunchKernelGGL(kfn, dim3(tiles), dim3(256), F32Cfg<32>::kLdsBytes, a.stream, static_cast<const float*>(a.A),
-                     static_cast<const float*>(a.B), static_cast<float*>(a.C), (int)a.m, (int)a.n, (int)a.k);
-  return hipGetLastError();
+  if (!f32_small_tiles(a.m, a.n, a.num_cus)) return launch_w4<4, kEdge, false>(a, SkPlan{0, 0, 1, 1});
+  const SkPlan p = f32_plan(a.m, a.n, a.k, a.num_cus);
+  return p.units > 0 ? launch_w4<2, kEdge, true>(a, p) : launch_w4<2, kEdge, false>(a, p);
+}
+
+// Workspace of versions 2 and 3: the split's counters and partials.
+size_t f32_workspace(size_t m, size_t n, size_t k, int num_cus) {
+  if (k % 32 != 0 || !f32_small_tiles(m, n, num_cus)) return 0;
+  const SkPlan p = f32_plan(m, n, k, num_cus);
+  return p.units > 0 ? kSkCounterBytes + (size_t)p.units * kF32SlotBytes : 0;
 }
 
 // 32-deep k-tiles when K allows (one barrier per 128 MFMAs of a wave:
@@ -617,8 +828,9 @@ void register_f32_mfma() {
   e.in_dtype = VK_DTYPE_F32;
   e.name = "f32_v2_mfma256";
   e.caps = make_caps(2, VK_DTYPE_F32, kOutF32, kBM, kBN, 16, 16, kBM, kBN, 32, 256, F32Cfg<32>::kLdsBytes, 0, 0);
+  e.caps.uses_workspace = 1;  // K split on grids of few tiles
   e.launch = launch_f32_mfma;
-  e.workspace = nullptr;
+  e.workspace = f32_workspace;
   e.shape_ok = f32_mfma_shape_ok;
   register_kernel(e);
 
@@ -626,6 +838,7 @@ void register_f32_mfma() {
   e3.version = 3;
   e3.name = "f32_v3_mfma256_edge";
   e3.caps = make_caps(3, VK_DTYPE_F32, kOutF32, 1, 4, 4, 16, kBM, kBN, 32, 256, F32Cfg<32>::kLdsBytes, 0, 0);
+  e3.caps.uses_workspace = 1;
   e3.launch = launch_f32_mfma_edge;
   e3.shape_ok = f32_mfma_edge_shape_ok;
   register_kernel(e3);

@@ -107,13 +107,15 @@ __host__ __device__ inline SkPlan sk_plan(int64_t T, int64_t I, int num_cus) {
 constexpr int kFillMinIters = 8;
 constexpr int kFillMaxPieces = 8;
 constexpr int kFillLastExtra = 1;
-__host__ __device__ inline SkPlan sk_plan_fill(int64_t T, int64_t I, int num_cus) {
+// min_iters: the fewest k-tiles per piece (the fp32 kernel's k-tiles take
+// ~2 us each, so it splits down to 4).
+__host__ __device__ inline SkPlan sk_plan_fill(int64_t T, int64_t I, int num_cus, int min_iters = kFillMinIters) {
   const SkPlan whole{(int)T, 0, 1, 1};
   const int64_t C = num_cus < kSkMaxUnits ? num_cus : kSkMaxUnits;
-  if (C <= 0 || T <= 0 || 2 * T > C) return whole;
+  if (C <= 0 || T <= 0 || 2 * T > C || min_iters < 1) return whole;
   int64_t s = C / T;
   if (s > kFillMaxPieces) s = kFillMaxPieces;
-  if (s > I / kFillMinIters) s = I / kFillMinIters;
+  if (s > I / min_iters) s = I / min_iters;
   if (s < 2) return whole;
   return SkPlan{0, (int)(s * T), (int)s, T % 8 == 0 ? 8 : 1};
 }
