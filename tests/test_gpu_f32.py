@@ -25,14 +25,16 @@ pytestmark = pytest.mark.gpu
 
 SHAPES_V1 = [(128, 128, 16), (256, 384, 64), (512, 512, 512), (1, 1, 1), (17, 33, 65), (130, 250, 70),
              (128, 256, 16), (256, 512, 32), (384, 768, 48), (1024, 512, 1024), (128, 256, 2000)]
-# (version 2, 256 CUs) 256 x 256 tiles: (4352, 4096, 64); 128 x 128 whole:
-# (512, 256, 64), (256, 256, 32), (2048, 2048, 128); split: (768, 512, 256)
-# in 2 pieces, (1024, 1024, 512), (512, 512, 512) and (1024, 1024, 1024) in
-# 4, (256, 256, 1024) in 8
+# (version 2, 256 CUs) 256 x 256 tiles: (4096, 4096, 64); 128 x 128 whole:
+# (512, 256, 64), (256, 256, 32), (2048, 2048, 128), (4352, 4096, 64) (272
+# tiles of 256 x 256 would take two rounds of the CUs); split: (1280, 1280,
+# 256) in 2 pieces, (768, 512, 256), (1024, 1024, 512) and (1024, 1024,
+# 1024) in 4, (512, 512, 512) and (256, 256, 1024) in 8
 SHAPES_V2 = [(256, 256, 16), (512, 256, 64), (256, 512, 48), (768, 512, 256), (1024, 1024, 512), (256, 256, 32),
-             (4352, 4096, 64), (512, 512, 512), (1024, 1024, 1024), (256, 256, 1024), (2048, 2048, 128)]
-# split edge tiles: (1000, 1000, 1024) 4 pieces, (300, 600, 2048) and
-# (129, 4, 512) 8 and 4
+             (4352, 4096, 64), (512, 512, 512), (1024, 1024, 1024), (256, 256, 1024), (2048, 2048, 128),
+             (4096, 4096, 64), (1280, 1280, 256)]
+# split edge tiles: (1000, 1000, 1024) in 4 pieces, (300, 600, 2048) and
+# (129, 4, 512) in 8
 SHAPES_V3 = [(1, 4, 4), (17, 36, 68), (300, 260, 100), (257, 512, 36), (1000, 1000, 1000), (256, 256, 64),
              (300, 260, 96), (257, 516, 64), (1000, 1000, 1024), (1, 4, 32), (300, 600, 2048), (129, 4, 512)]
 CASES = [(1, s) for s in SHAPES_V1] + [(2, s) for s in SHAPES_V2] + [(3, s) for s in SHAPES_V3]
@@ -97,7 +99,7 @@ def test_f32_4096(gpu, oracle, version):
 
 def test_f32_mfma_repeat_deterministic(gpu):
     """20 launches of version 2 with C poisoned before each: bitwise equal
-    (48 tiles of 128 x 128, K split in 4: whichever piece arrives last, the
+    (48 tiles of 128 x 128, K split in 5: whichever piece arrives last, the
     pieces are summed in k order)."""
     import torch
     import vibekernel_amd as vk

@@ -312,7 +312,8 @@ extern "C" int vk_timeline_f32_read(unsigned long long* host, int waves) {
 // (kNB x kNB blocks of 32x32); wave w owns rows 32 kNB (w / 2) and columns
 // 32 kNB (w % 2) onward.
 //  * kNB = 4, 256x256 tiles (256 fp32 accumulators per lane in AGPRs), where
-//    those tiles give every CU one: per k-tile a wave reads 16 KB of A and
+//    those tiles fill the CUs in as few waves as 128x128 ones: per k-tile a
+//    wave reads 16 KB of A and
 //    16 KB of B fragments (the eight-wave kernel's waves 16 + 8 KB each, two
 //    per SIMD), a third less LDS data per MFMA.  Measured per k-tile
 //    (timeline build, 4096^3): 17,113 shader cycles against the 16,384 its
@@ -320,13 +321,17 @@ extern "C" int vk_timeline_f32_read(unsigned long long* host, int waves) {
 //    fragment reads took 16,420 (the A reads' 16 ds_read_b128 cost ~510
 //    cycles, the B reads' 32 ds_read2st64_b32 ~225), without the loads
 //    16,988, without the barrier 17,090.
-//  * kNB = 2, 128x128 tiles (64 accumulators per lane), for grids whose
-//    256x256 tiles would leave CUs idle (1024^3: 16 of them on 256 CUs):
-//    four times as many tiles, and where even those fill at most half of
+//  * kNB = 2, 128x128 tiles (64 accumulators per lane) everywhere else:
+//    four times as many tiles, for grids whose 256x256 tiles would leave
+//    CUs idle (1024^3: 16 of them on 256 CUs) or fill a last wave in part
+//    (4096 x 4352: 272); where even the 128x128 tiles fill at most half of
 //    the CUs, K is split over the idle ones (kSplit, below).  An fp32 MFMA
 //    takes 64 cycles, so a wave's 128x128x32 k-tile is 4096 cycles of MFMA
 //    against 16 KB of fragment reads and 8 KB of loads: the smaller tile
-//    costs the matrix cores nothing.
+//    costs the matrix cores next to nothing (measured at 4096^3, 2 rounds on
+//    one box: 943.8 / 945.3 us per launch against 939.9 / 941.7 with
+//    256x256 tiles; 4096 x 4352 x 4096 1188 / 1193 against 1873 / 1861;
+//    6144 x 4096 x 4096 1416 / 1417 against 1900 / 1881).
 // A wave's fragments are read one group of 4 steps ahead into a second
 // register set: the next group's kReads reads (kNB A reads of 16 bytes, 2 kNB
 // pairs of B values) one after each of the first kReads MFMAs from the
@@ -366,17 +371,23 @@ struct F32W4 {
 // and increments the counter, and the one that sees np - 1 is the last.  The
 // last sums P0 + P1 + ... in k order (its own piece from registers), so C
 // does not depend on the arrival order, stores C and resets the counter.
-// A piece of 4 k-tiles is ~8 us of MFMA at the board's clock, twice the
-// hand-off (its partial published, then read back by the last arrival).
-constexpr int kF32MinIters = 4;
+// A piece of 2 k-tiles is ~3.5 us of MFMA at the board's clock.  Measured
+// against pieces of at least 4 (2 rounds, one box, us per launch): 512^3
+// 15.5 against 16.7, 512 x 512 x 256 12.8 against 15.0, 256 x 512 x 512
+// 15.2 against 16.6.
+constexpr int kF32MinIters = 2;
 constexpr size_t kF32SlotBytes = (size_t)128 * 128 * sizeof(float);  // one tile's fp32 partial
 constexpr uint32_t kF32WaveBytes = 64 * 64 * sizeof(float);          // a wave's 64x64 quarter
 
 __host__ __device__ inline int64_t f32_tiles(size_t m, size_t n, size_t t) {
   return (int64_t)((m + t - 1) / t) * (int64_t)((n + t - 1) / t);
 }
-// 128x128 tiles where the 256x256 ones leave CUs without a tile.
-inline bool f32_small_tiles(size_t m, size_t n, int num_cus) { return f32_tiles(m, n, 256) < num_cus; }
+// 128x128 tiles unless the 256x256 ones, each four times the work, fill the
+// CUs in as few rounds (4096^3: 256 tiles in one round against 1024 in four).
+inline bool f32_small_tiles(size_t m, size_t n, int num_cus) {
+  const int64_t c = num_cus > 0 ? num_cus : 1;
+  return 4 * ((f32_tiles(m, n, 256) + c - 1) / c) > (f32_tiles(m, n, 128) + c - 1) / c;
+}
 inline SkPlan f32_plan(size_t m, size_t n, size_t k, int num_cus) {
   return sk_plan_fill(f32_tiles(m, n, 128), (int64_t)(k / 32), num_cus, kF32MinIters);
 }
@@ -767,8 +778,9 @@ hipError_t launch_w4(const GemmArgs& a, const SkPlan& p) {
   return hipGetLastError();
 }
 
-// 256x256 tiles where they give every CU one; otherwise 128x128 tiles, with
-// K split where those fill at most half of the CUs.
+// 256x256 tiles where they take as few rounds of the CUs as 128x128 ones;
+// otherwise 128x128 tiles, with K split where those fill at most half of the
+// CUs.
 template <bool kEdge>
 hipError_t launch_f32_mfma4(const GemmArgs& a) {
   if (!f32_small_tiles(a.m, a.n, a.num_cus)) return launch_w4<4, kEdge, false>(a, SkPlan{0, 0, 1, 1});

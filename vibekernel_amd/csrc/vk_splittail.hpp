@@ -108,7 +108,7 @@ constexpr int kFillMinIters = 8;
 constexpr int kFillMaxPieces = 8;
 constexpr int kFillLastExtra = 1;
 // min_iters: the fewest k-tiles per piece (the fp32 kernel's k-tiles take
-// ~2 us each, so it splits down to 4).
+// ~1.7 us each, so it splits down to 2).
 __host__ __device__ inline SkPlan sk_plan_fill(int64_t T, int64_t I, int num_cus, int min_iters = kFillMinIters) {
   const SkPlan whole{(int)T, 0, 1, 1};
   const int64_t C = num_cus < kSkMaxUnits ? num_cus : kSkMaxUnits;
