@@ -140,7 +140,8 @@ def test_f32_split_workspace_follows_shape():
         assert _abi.workspace_bytes(v, f32, 4096, 4352, 4096) == 0   # 1088 tiles of 128 x 128: whole
         assert _abi.workspace_bytes(v, f32, 256, 256, 32) == 0       # one k-tile
         assert _abi.workspace_bytes(v, f32, 256, 256, 1024) == 8192 + 32 * 65536     # 4 tiles x 8 pieces
-        assert _abi.workspace_bytes(v, f32, 1024, 1024, 1040) == 0   # K % 32 != 0: the eight-wave kernel
+        assert _abi.workspace_bytes(v, f32, 4096, 4096, 1040) == 0   # 256 tiles of 256 x 256 (eight-wave kernel)
+        assert _abi.workspace_bytes(v, f32, 1024, 1024, 1040) == 8192 + 256 * 65536  # 33 k-tiles, the last masked
     assert _abi.workspace_bytes(3, f32, 1000, 1000, 1024) == 8192 + 256 * 65536  # 64 edge tiles x 4 pieces
     assert _abi.workspace_bytes(3, f32, 300, 260, 96) == 0           # 3 k-tiles: too shallow to split
     assert _abi.workspace_bytes(3, f32, 300, 260, 128) == 8192 + 18 * 65536     # 9 tiles x 2 pieces

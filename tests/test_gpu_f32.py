@@ -6,13 +6,14 @@
 * version 2 (matrix cores, v_mfma_f32_32x32x2_f32, two products per step;
   the four-wave kernel when K % 32 == 0 -- 256 x 256 tiles where they give
   every CU one, else 128 x 128 tiles, K split over idle CUs where those fill
-  at most half of them -- the eight-wave one with 16-deep k-tiles
-  otherwise): integer inputs exact; random inputs within 2 k u |A||B| of
+  at most half of them; K % 32 == 16 on 256 x 256 tiles: the eight-wave
+  kernel with 16-deep k-tiles): integer inputs exact; random inputs within 2 k u |A||B| of
   the exact (fp64) product; bitwise repeatable launch to launch (a split
   shape); shapes include one k-tile (K = 32), more tiles than CUs, 128 x 128
   tiles whole and split into 2 to 8 pieces;
 * version 3 (version 2 with masked edges: any M, N and K multiples of 4; the
-  four-wave kernel when K % 32 == 0): the same bars on ragged shapes,
+  four-wave kernel when K % 32 == 0 or on 128 x 128 tiles, the last k-tile
+  then masked per lane): the same bars on ragged shapes,
   bitwise equal to version 2 on its grid, nothing written outside C, and the
   values past an edge in memory never reach C.
 """
@@ -30,13 +31,18 @@ SHAPES_V1 = [(128, 128, 16), (256, 384, 64), (512, 512, 512), (1, 1, 1), (17, 33
 # tiles of 256 x 256 would take two rounds of the CUs); split: (1280, 1280,
 # 256) in 2 pieces, (768, 512, 256), (1024, 1024, 512) and (1024, 1024,
 # 1024) in 4, (512, 512, 512) and (256, 256, 1024) in 8
+# 4096 x 4096 x 48: the eight-wave kernel; (256, 256, 16), (256, 512, 48):
+# 128 x 128 tiles with the last k-tile masked
 SHAPES_V2 = [(256, 256, 16), (512, 256, 64), (256, 512, 48), (768, 512, 256), (1024, 1024, 512), (256, 256, 32),
              (4352, 4096, 64), (512, 512, 512), (1024, 1024, 1024), (256, 256, 1024), (2048, 2048, 128),
-             (4096, 4096, 64), (1280, 1280, 256)]
+             (4096, 4096, 64), (1280, 1280, 256), (4096, 4096, 48)]
 # split edge tiles: (1000, 1000, 1024) in 4 pieces, (300, 600, 2048) and
-# (129, 4, 512) in 8
+# (129, 4, 512) in 8; the k mask on 128 x 128 tiles: (1000, 1000, 1000) in
+# 4 pieces, (300, 260, 100) in 2, (17, 36, 68) whole; 4096 x 4096 x 100: the
+# eight-wave kernel with its mask
 SHAPES_V3 = [(1, 4, 4), (17, 36, 68), (300, 260, 100), (257, 512, 36), (1000, 1000, 1000), (256, 256, 64),
-             (300, 260, 96), (257, 516, 64), (1000, 1000, 1024), (1, 4, 32), (300, 600, 2048), (129, 4, 512)]
+             (300, 260, 96), (257, 516, 64), (1000, 1000, 1024), (1, 4, 32), (300, 600, 2048), (129, 4, 512),
+             (4096, 4096, 100)]
 CASES = [(1, s) for s in SHAPES_V1] + [(2, s) for s in SHAPES_V2] + [(3, s) for s in SHAPES_V3]
 
 

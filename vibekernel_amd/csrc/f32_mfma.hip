@@ -389,7 +389,7 @@ inline bool f32_small_tiles(size_t m, size_t n, int num_cus) {
   return 4 * ((f32_tiles(m, n, 256) + c - 1) / c) > (f32_tiles(m, n, 128) + c - 1) / c;
 }
 inline SkPlan f32_plan(size_t m, size_t n, size_t k, int num_cus) {
-  return sk_plan_fill(f32_tiles(m, n, 128), (int64_t)(k / 32), num_cus, kF32MinIters);
+  return sk_plan_fill(f32_tiles(m, n, 128), (int64_t)((k + 31) / 32), num_cus, kF32MinIters);
 }
 
 // Vector v of a wave's accumulators: block (v / 4kNB, (v / 4) % kNB),
@@ -483,8 +483,14 @@ __device__ __forceinline__ void f32_split_sum(float16v_ (&acc)[kNB][kNB], int np
 }
 
 // kSplit: this workgroup is unit blockIdx.x of the split plan {0, units,
-// pieces, chunks}; part and counters are the workspace.
-template <int kNB, bool kEdge, bool kSplit>
+// pieces, chunks}; part and counters are the workspace.  kKMask (with kEdge,
+// for K % 32 != 0): the last k-tile reaches past K.  B's k-rows past K read
+// zeros (the buffer range); A's k past K in memory are the next row's
+// values, which must not meet those zeros (an infinity would make a NaN), so
+// an A load whose chunk starts at or past K takes the matrix size as its
+// offset and reads zeros (K % 4 == 0: a 16-byte chunk lies wholly on one
+// side).
+template <int kNB, bool kEdge, bool kSplit, bool kKMask = false>
 __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict__ A, const float* __restrict__ B,
                                                         float* __restrict__ C, int M, int N, int K, int units,
                                                         int pieces, int chunks, float* __restrict__ part,
@@ -493,12 +499,13 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
   constexpr int BK = W::BK, kT = W::kT, kQ = W::kQ;
   constexpr int kDA = W::kDA, kDB = W::kDB, kD = W::kD;
   static_assert(!kSplit || kNB == 2, "K is split on the 128x128 tiles only");
+  static_assert(!kKMask || (kEdge && kNB == 2), "the k mask is for the 128x128 edge tiles");
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wr = wave >> 1, wc = wave & 1;
   const int tiles_m = (M + (kEdge ? kT - 1 : 0)) / kT, tiles_n = (N + (kEdge ? kT - 1 : 0)) / kT;
-  const int iters = K / BK;
+  const int iters = (K + (kKMask ? BK - 1 : 0)) / BK;
   int tm, tn, kb = 0, nk = iters;
   SkWork w{};
   if constexpr (kSplit) {
@@ -521,12 +528,14 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
   constexpr int kRowsPerDma = 1024 / (4 * BK);
   constexpr int kBLanesPerRow = 64 / W::kBRowsPerDma;
   uint32_t voffA[kDA], voffB[kDB];
+  uint32_t achunk = 0;  // kKMask: bits 3d .. 3d + 2, the k-chunk A load d fetches
 #pragma unroll
   for (int d = 0; d < kDA; d++) {
     const int i = kDA * wave + d;
     const int row = kRowsPerDma * i + lane / W::kRowChunks;
     const int ca = (lane % W::kRowChunks) ^ swz_a32<BK>(row);
     voffA[d] = (uint32_t)(((size_t)row * K + ca * 4) * 4);
+    achunk |= (uint32_t)ca << (3 * d);
   }
 #pragma unroll
   for (int d = 0; d < kDB; d++) {
@@ -545,12 +554,17 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
   auto issue_one = [&](int kt, int slot, int d) {
     const uint32_t s = lds_base + slot * W::kStageBytes;
     if constexpr (kEdge) {
-      // K % 32 == 0: only rows past M and columns past N; the buffer ranges
-      // give zeros past each matrix (B columns past N read the next row's,
-      // feeding only C columns that are not stored)
-      if (d < kDA)
-        dma16_buf(rsrcA, voffA[d], (uint32_t)(m0 * K + (kb + kt) * BK) * 4u, s + (kDA * wave + d) * 1024);
-      else
+      // rows past M and k-rows past K read zeros (the buffer ranges); B
+      // columns past N read the next row's, feeding only C columns that are
+      // not stored
+      if (d < kDA) {
+        uint32_t off = voffA[d];
+        if constexpr (kKMask) {
+          const int kleft = K - (kb + kt) * BK;
+          off = 4 * (int)((achunk >> (3 * d)) & 7u) < kleft ? off : sizeA;  // sizeA: zeros
+        }
+        dma16_buf(rsrcA, off, (uint32_t)(m0 * K + (kb + kt) * BK) * 4u, s + (kDA * wave + d) * 1024);
+      } else
         dma16_buf(rsrcB, voffB[d - kDA], (uint32_t)((kb + kt) * BK * N + n0) * 4u,
                   s + W::kABytes + (kDB * wave + d - kDA) * 1024);
     } else {
@@ -754,11 +768,11 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
 #endif
 }
 
-template <int kNB, bool kEdge, bool kSplit>
+template <int kNB, bool kEdge, bool kSplit, bool kKMask = false>
 hipError_t launch_w4(const GemmArgs& a, const SkPlan& p) {
   using W = F32W4<kNB>;
   static std::atomic<uint64_t> attr_done{0};
-  auto kfn = f32_mfma4_kernel<kNB, kEdge, kSplit>;
+  auto kfn = f32_mfma4_kernel<kNB, kEdge, kSplit, kKMask>;
   hipError_t e = ensure_lds_attr(kfn, W::kLdsBytes, a.device, attr_done);
   if (e != hipSuccess) return e;
   unsigned* counters = nullptr;
@@ -778,19 +792,23 @@ hipError_t launch_w4(const GemmArgs& a, const SkPlan& p) {
   return hipGetLastError();
 }
 
-// 256x256 tiles where they take as few rounds of the CUs as 128x128 ones;
-// otherwise 128x128 tiles, with K split where those fill at most half of the
-// CUs.
+bool f32_mfma_edge_shape_ok(size_t m, size_t n, size_t k);
+
+// The 128x128 tiles (f32_small_tiles), K split where they fill at most half
+// of the CUs; K % 32 != 0 through the edge kernel with the k mask (also on
+// version 2's grid, whose 16-deep eight-wave kernel has 256x256 tiles only;
+// the caller checks the edge kernel's size limits).
 template <bool kEdge>
-hipError_t launch_f32_mfma4(const GemmArgs& a) {
-  if (!f32_small_tiles(a.m, a.n, a.num_cus)) return launch_w4<4, kEdge, false>(a, SkPlan{0, 0, 1, 1});
+hipError_t launch_f32_small(const GemmArgs& a) {
   const SkPlan p = f32_plan(a.m, a.n, a.k, a.num_cus);
+  if (a.k % 32 != 0)
+    return p.units > 0 ? launch_w4<2, true, true, true>(a, p) : launch_w4<2, true, false, true>(a, p);
   return p.units > 0 ? launch_w4<2, kEdge, true>(a, p) : launch_w4<2, kEdge, false>(a, p);
 }
 
 // Workspace of versions 2 and 3: the split's counters and partials.
 size_t f32_workspace(size_t m, size_t n, size_t k, int num_cus) {
-  if (k % 32 != 0 || !f32_small_tiles(m, n, num_cus)) return 0;
+  if (!f32_small_tiles(m, n, num_cus) || (k % 32 != 0 && !f32_mfma_edge_shape_ok(m, n, k))) return 0;
   const SkPlan p = f32_plan(m, n, k, num_cus);
   return p.units > 0 ? kSkCounterBytes + (size_t)p.units * kF32SlotBytes : 0;
 }
@@ -810,7 +828,14 @@ hipError_t launch_bk(const GemmArgs& a) {
   return hipGetLastError();
 }
 
-hipError_t launch_f32_mfma(const GemmArgs& a) { return a.k % 32 == 0 ? launch_f32_mfma4<false>(a) : launch_bk<16>(a); }
+// 256x256 tiles where they take as few rounds of the CUs as 128x128 ones
+// (the four-wave kernel when K % 32 == 0, else the eight-wave one with
+// 16-deep k-tiles), otherwise the 128x128 tiles.
+hipError_t launch_f32_mfma(const GemmArgs& a) {
+  if (f32_small_tiles(a.m, a.n, a.num_cus) && (a.k % 32 == 0 || f32_mfma_edge_shape_ok(a.m, a.n, a.k)))
+    return launch_f32_small<false>(a);
+  return a.k % 32 == 0 ? launch_w4<4, false, false>(a, SkPlan{0, 0, 1, 1}) : launch_bk<16>(a);
+}
 
 // 32-bit lane offsets: the rows of A one instruction covers span less than
 // 256 * K floats beyond the k-tile base and the k-rows of B 32 * N floats;
@@ -824,7 +849,8 @@ bool f32_mfma_shape_ok(size_t m, size_t n, size_t k) {
 // masked where K % 32 != 0); each operand below 2^31 bytes (buffer sizes and
 // offsets).
 hipError_t launch_f32_mfma_edge(const GemmArgs& a) {
-  return a.k % 32 == 0 ? launch_f32_mfma4<true>(a) : launch_bk<32, true>(a);
+  if (f32_small_tiles(a.m, a.n, a.num_cus)) return launch_f32_small<true>(a);
+  return a.k % 32 == 0 ? launch_w4<4, true, false>(a, SkPlan{0, 0, 1, 1}) : launch_bk<32, true>(a);
 }
 
 bool f32_mfma_edge_shape_ok(size_t m, size_t n, size_t k) {
