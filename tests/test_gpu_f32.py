@@ -1,7 +1,8 @@
 """GPU parity of the fp32 kernels against the oracle's cblas_sgemm restatement
 (matmul_f32_v0_cblas.cpp:8-12), through the C ABI.
 
-* version 1 (VALU, one fmaf per term in ascending k): equal to the oracle,
+* version 1 (VALU, one fmaf per term in ascending k; 128 x 256 tiles, or
+  64 x 64 where those fill the CUs in fewer rounds): equal to the oracle,
   bit for bit, on every shape;
 * version 2 (matrix cores, v_mfma_f32_32x32x2_f32, two products per step;
   the four-wave kernel when K % 32 == 0 -- 256 x 256 tiles where they give
@@ -24,8 +25,12 @@ from gpu_util import announce, make_inputs
 
 pytestmark = pytest.mark.gpu
 
+# version 1 on 256 CUs: 64 x 64 tiles for every shape here but the last two
+# (the bounds-checked 128 x 256 kernel at 4000 x 4000, the asm kernel at
+# 4096 x 4096)
 SHAPES_V1 = [(128, 128, 16), (256, 384, 64), (512, 512, 512), (1, 1, 1), (17, 33, 65), (130, 250, 70),
-             (128, 256, 16), (256, 512, 32), (384, 768, 48), (1024, 512, 1024), (128, 256, 2000)]
+             (128, 256, 16), (256, 512, 32), (384, 768, 48), (1024, 512, 1024), (128, 256, 2000),
+             (4000, 4000, 40), (4096, 4096, 32)]
 # (version 2, 256 CUs) 256 x 256 tiles: (4096, 4096, 64); 128 x 128 whole:
 # (512, 256, 64), (256, 256, 32), (2048, 2048, 128), (4352, 4096, 64) (272
 # tiles of 256 x 256 would take two rounds of the CUs); split: (1280, 1280,

@@ -12,7 +12,9 @@
 //   * tile-divisible shapes: the k-loop as one asm block with hand-chosen
 //     registers, k-tiles staged by direct-to-LDS loads (f32_valu_asm_kernel);
 //   * any other shape: a C++ kernel with bounds checks, the next k-tile
-//     prefetched into registers and stored into LDS (A transposed, k-major).
+//     prefetched into registers and stored into LDS (A transposed, k-major);
+//     on grids of few 128x256 tiles the same kernel on 64x64 tiles (4x4
+//     outputs per thread) fills more CUs.
 // Roofline: the VOP2 FMA (`v_fmac_f32_e32`) runs at the full 157.3 TFLOP/s
 // rate on MI355X (measured 146.7 on independent chains; the VOP3 form runs
 // at half), unless its three VGPR operands share a register bank, which
@@ -35,11 +37,17 @@ constexpr int kLdA = kTM * kBK / 4 / 256;  // float4 loads of A per thread per k
 constexpr int kLdB = kBK * kTN / 4 / 256;  // float4 loads of B per thread per k-tile
 static_assert(kLdA == 2 && kLdB == 4, "tile load mapping");
 
-template <bool kCheck>
+// kRB row blocks of 64 and kNG column groups of 64 per tile: 128x256 (the
+// asm kernel's tile) or, for grids of few such tiles, 64x64 (4x4 outputs per
+// thread), with the same per-element order.
+template <bool kCheck, int kRB = 2, int kNG = kCG>
 __global__ __launch_bounds__(256) void f32_valu_kernel(const float* __restrict__ A,
                                                        const float* __restrict__ B,
                                                        float* __restrict__ C, int64_t M, int64_t N,
                                                        int64_t K) {
+  constexpr int kTM = 64 * kRB, kTN = 64 * kNG, kApitch = kTM + 4;
+  constexpr int kLdA = kTM * kBK / 4 / 256, kLdB = kBK * kTN / 4 / 256;
+  static_assert(kLdA * 1024 == kTM * kBK && kLdB * 1024 == kBK * kTN, "whole float4 loads per thread");
   __shared__ __attribute__((aligned(16))) float As[2][kBK * kApitch];
   __shared__ __attribute__((aligned(16))) float Bs[2][kBK * kTN];
 
@@ -48,7 +56,7 @@ __global__ __launch_bounds__(256) void f32_valu_kernel(const float* __restrict__
   const int64_t m0 = (int64_t)blockIdx.y * kTM;
   const int64_t n0 = (int64_t)blockIdx.x * kTN;
 
-  // Global load mapping: A: 128 rows x BK/4 float4 per row; B: BK rows x TN/4 float4.
+  // Global load mapping: A: TM rows x BK/4 float4 per row; B: BK rows x TN/4 float4.
   constexpr int kC4A = kBK / 4;   // float4 per A row
   constexpr int kC4B = kTN / 4;   // float4 per B row
   float4v ra[kLdA], rb[kLdB];
@@ -96,11 +104,11 @@ __global__ __launch_bounds__(256) void f32_valu_kernel(const float* __restrict__
     }
   };
 
-  float acc[8][4 * kCG];
+  float acc[4 * kRB][4 * kNG];
 #pragma unroll
-  for (int i = 0; i < 8; i++)
+  for (int i = 0; i < 4 * kRB; i++)
 #pragma unroll
-    for (int j = 0; j < 4 * kCG; j++) acc[i][j] = 0.0f;
+    for (int j = 0; j < 4 * kNG; j++) acc[i][j] = 0.0f;
 
   const int64_t nk = (K + kBK - 1) / kBK;
   load_tile(0);
@@ -111,20 +119,24 @@ __global__ __launch_bounds__(256) void f32_valu_kernel(const float* __restrict__
     if (kt + 1 < nk) load_tile((kt + 1) * kBK);
 #pragma unroll 2
     for (int kk = 0; kk < kBK; kk++) {
-      const float4v a0 = *reinterpret_cast<const float4v*>(&As[cur][kk * kApitch + ty * 4]);
-      const float4v a1 = *reinterpret_cast<const float4v*>(&As[cur][kk * kApitch + 64 + ty * 4]);
-      float a[8] = {a0[0], a0[1], a0[2], a0[3], a1[0], a1[1], a1[2], a1[3]};
-      float b[4 * kCG];
+      float a[4 * kRB];
 #pragma unroll
-      for (int g = 0; g < kCG; g++) {
+      for (int r = 0; r < kRB; r++) {
+        const float4v ar = *reinterpret_cast<const float4v*>(&As[cur][kk * kApitch + 64 * r + ty * 4]);
+#pragma unroll
+        for (int q = 0; q < 4; q++) a[4 * r + q] = ar[q];
+      }
+      float b[4 * kNG];
+#pragma unroll
+      for (int g = 0; g < kNG; g++) {
         const float4v bg = *reinterpret_cast<const float4v*>(&Bs[cur][kk * kTN + 64 * g + tx * 4]);
 #pragma unroll
         for (int q = 0; q < 4; q++) b[4 * g + q] = bg[q];
       }
 #pragma unroll
-      for (int i = 0; i < 8; i++)
+      for (int i = 0; i < 4 * kRB; i++)
 #pragma unroll
-        for (int j = 0; j < 4 * kCG; j++) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
+        for (int j = 0; j < 4 * kNG; j++) acc[i][j] = __builtin_fmaf(a[i], b[j], acc[i][j]);
     }
     if (kt + 1 < nk) {
       store_tile(cur ^ 1);
@@ -133,10 +145,10 @@ __global__ __launch_bounds__(256) void f32_valu_kernel(const float* __restrict__
   }
 
 #pragma unroll
-  for (int i = 0; i < 8; i++) {
-    const int64_t row = m0 + (i < 4 ? ty * 4 + i : 64 + ty * 4 + (i - 4));
+  for (int i = 0; i < 4 * kRB; i++) {
+    const int64_t row = m0 + 64 * (i / 4) + ty * 4 + i % 4;
 #pragma unroll
-    for (int g = 0; g < kCG; g++) {
+    for (int g = 0; g < kNG; g++) {
       const int64_t col = n0 + g * 64 + tx * 4;
       if (!kCheck) {
         float4v v = {acc[i][g * 4 + 0], acc[i][g * 4 + 1], acc[i][g * 4 + 2], acc[i][g * 4 + 3]};
@@ -413,11 +425,29 @@ __global__ __launch_bounds__(256) void f32_valu_asm_kernel(const float* __restri
 }
 #pragma clang diagnostic pop
 
+// 64x64 tiles where the 128x256 ones, eight times the work each, need more
+// rounds of the CUs for the same work (512^3: 8 tiles on 256 CUs).  Measured
+// (us per launch, 2 rounds, one box, against the 128x256 kernels): 512^3
+// 43.2 against 131.3, 1024^3 83.5 / 260.0, 1536^3 203.6 / 386.8, 2048^3
+// 376.2 / 514.7, 4096 x 1024 x 4096 737.4 / 1024.9; a 128x128 tile (8x8
+// outputs per thread) was slower than 64x64 on each of them (2048^3 420.5).
+bool f32_valu_small(size_t m, size_t n, int num_cus) {
+  const int64_t c = num_cus > 0 ? num_cus : 1;
+  const int64_t big = (int64_t)((m + kTM - 1) / kTM) * (int64_t)((n + kTN - 1) / kTN);
+  const int64_t small = (int64_t)((m + 63) / 64) * (int64_t)((n + 63) / 64);
+  return 8 * ((big + c - 1) / c) > (small + c - 1) / c && (m + 63) / 64 <= 65535;
+}
+
 hipError_t launch_f32(const GemmArgs& a) {
-  dim3 grid((unsigned)((a.n + kTN - 1) / kTN), (unsigned)((a.m + kTM - 1) / kTM));
   const float* A = static_cast<const float*>(a.A);
   const float* B = static_cast<const float*>(a.B);
   float* C = static_cast<float*>(a.C);
+  if (f32_valu_small(a.m, a.n, a.num_cus)) {
+    hipLaunchKernelGGL((f32_valu_kernel<true, 1, 1>), dim3((unsigned)((a.n + 63) / 64), (unsigned)((a.m + 63) / 64)),
+                       dim3(256), 0, a.stream, A, B, C, (int64_t)a.m, (int64_t)a.n, (int64_t)a.k);
+    return hipGetLastError();
+  }
+  dim3 grid((unsigned)((a.n + kTN - 1) / kTN), (unsigned)((a.m + kTM - 1) / kTM));
   const bool full = a.m % kTM == 0 && a.n % kTN == 0 && a.k % kBK == 0 &&
                     ((uintptr_t)A & 15) == 0 && ((uintptr_t)B & 15) == 0 &&
                     ((uintptr_t)C & 15) == 0 && asm_offsets_fit(a.m, a.n, a.k);
