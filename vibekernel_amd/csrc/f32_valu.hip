@@ -37,14 +37,17 @@ constexpr int kLdA = kTM * kBK / 4 / 256;  // float4 loads of A per thread per k
 constexpr int kLdB = kBK * kTN / 4 / 256;  // float4 loads of B per thread per k-tile
 static_assert(kLdA == 2 && kLdB == 4, "tile load mapping");
 
-// kRB row blocks of 64 and kNG column groups of 64 per tile: 128x256 (the
-// asm kernel's tile) or, for grids of few such tiles, 64x64 (4x4 outputs per
-// thread), with the same per-element order.
-template <bool kCheck, int kRB = 2, int kNG = kCG>
+// kRB row blocks of 64 and kNG column groups of 64 per tile, kKT-deep
+// k-tiles: 128x256x16 (the asm kernel's tile) or, for grids of few such
+// tiles, 64x64x32 (4x4 outputs per thread, 4 k-steps per unrolled loop body),
+// with the same per-element order.
+template <bool kCheck, int kRB = 2, int kNG = kCG, int kKT = vk::kBK>
 __global__ __launch_bounds__(256) void f32_valu_kernel(const float* __restrict__ A,
                                                        const float* __restrict__ B,
                                                        float* __restrict__ C, int64_t M, int64_t N,
                                                        int64_t K) {
+  constexpr int kBK = kKT;  // k-tile depth
+  constexpr int kUnroll = kRB * kNG == 1 ? 4 : 2;  // k-steps per unrolled loop body
   constexpr int kTM = 64 * kRB, kTN = 64 * kNG, kApitch = kTM + 4;
   constexpr int kLdA = kTM * kBK / 4 / 256, kLdB = kBK * kTN / 4 / 256;
   static_assert(kLdA * 1024 == kTM * kBK && kLdB * 1024 == kBK * kTN, "whole float4 loads per thread");
@@ -117,7 +120,7 @@ __global__ __launch_bounds__(256) void f32_valu_kernel(const float* __restrict__
   for (int64_t kt = 0; kt < nk; kt++) {
     const int cur = (int)(kt & 1);
     if (kt + 1 < nk) load_tile((kt + 1) * kBK);
-#pragma unroll 2
+#pragma unroll kUnroll
     for (int kk = 0; kk < kBK; kk++) {
       float a[4 * kRB];
 #pragma unroll
@@ -431,6 +434,11 @@ __global__ __launch_bounds__(256) void f32_valu_asm_kernel(const float* __restri
 // 43.2 against 131.3, 1024^3 83.5 / 260.0, 1536^3 203.6 / 386.8, 2048^3
 // 376.2 / 514.7, 4096 x 1024 x 4096 737.4 / 1024.9; a 128x128 tile (8x8
 // outputs per thread) was slower than 64x64 on each of them (2048^3 420.5).
+// With one wave per SIMD the small tile waits on its loads and LDS reads:
+// 32-deep k-tiles and 4 k-steps per loop body took it further (512^3 35.5,
+// 1024^3 69.7, 2048^3 281.8; 48-deep 42.9 / 84.1 / 359.7, 32-deep with 2
+// k-steps per body 39.8 / 78.0 / 278.5, fully unrolled 37.5 / 78.8 /
+// 605.5).
 bool f32_valu_small(size_t m, size_t n, int num_cus) {
   const int64_t c = num_cus > 0 ? num_cus : 1;
   const int64_t big = (int64_t)((m + kTM - 1) / kTM) * (int64_t)((n + kTN - 1) / kTN);
@@ -443,7 +451,7 @@ hipError_t launch_f32(const GemmArgs& a) {
   const float* B = static_cast<const float*>(a.B);
   float* C = static_cast<float*>(a.C);
   if (f32_valu_small(a.m, a.n, a.num_cus)) {
-    hipLaunchKernelGGL((f32_valu_kernel<true, 1, 1>), dim3((unsigned)((a.n + 63) / 64), (unsigned)((a.m + 63) / 64)),
+    hipLaunchKernelGGL((f32_valu_kernel<true, 1, 1, 32>), dim3((unsigned)((a.n + 63) / 64), (unsigned)((a.m + 63) / 64)),
                        dim3(256), 0, a.stream, A, B, C, (int64_t)a.m, (int64_t)a.n, (int64_t)a.k);
     return hipGetLastError();
   }
