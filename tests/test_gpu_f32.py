@@ -37,17 +37,20 @@ SHAPES_V1 = [(128, 128, 16), (256, 384, 64), (512, 512, 512), (1, 1, 1), (17, 33
 # 256) in 2 pieces, (768, 512, 256), (1024, 1024, 512) and (1024, 1024,
 # 1024) in 4, (512, 512, 512) and (256, 256, 1024) in 8
 # 4096 x 4096 x 48: the eight-wave kernel; (256, 256, 16), (256, 512, 48):
-# 128 x 128 tiles with the last k-tile masked
+# 128 x 128 tiles with the last k-tile masked; (2304, 2048, 2048): 256 whole
+# tiles and 32 in a tail split in 4; (2304, 2304, 2048): 68 in a tail split
+# in 3, one chunk
 SHAPES_V2 = [(256, 256, 16), (512, 256, 64), (256, 512, 48), (768, 512, 256), (1024, 1024, 512), (256, 256, 32),
              (4352, 4096, 64), (512, 512, 512), (1024, 1024, 1024), (256, 256, 1024), (2048, 2048, 128),
-             (4096, 4096, 64), (1280, 1280, 256), (4096, 4096, 48)]
+             (4096, 4096, 64), (1280, 1280, 256), (4096, 4096, 48), (2304, 2048, 2048),
+             (2304, 2304, 2048)]
 # split edge tiles: (1000, 1000, 1024) in 4 pieces, (300, 600, 2048) and
 # (129, 4, 512) in 8; the k mask on 128 x 128 tiles: (1000, 1000, 1000) in
 # 4 pieces, (300, 260, 100) in 2, (17, 36, 68) whole; 4096 x 4096 x 100: the
-# eight-wave kernel with its mask
+# eight-wave kernel with its mask; (2100, 2000, 2048): a split tail
 SHAPES_V3 = [(1, 4, 4), (17, 36, 68), (300, 260, 100), (257, 512, 36), (1000, 1000, 1000), (256, 256, 64),
              (300, 260, 96), (257, 516, 64), (1000, 1000, 1024), (1, 4, 32), (300, 600, 2048), (129, 4, 512),
-             (4096, 4096, 100)]
+             (4096, 4096, 100), (2100, 2000, 2048)]
 CASES = [(1, s) for s in SHAPES_V1] + [(2, s) for s in SHAPES_V2] + [(3, s) for s in SHAPES_V3]
 
 
@@ -143,7 +146,8 @@ def test_f32_mfma_rejects_unaligned_shape(gpu):
 def test_f32_edge_on_grid_equals_v2(gpu):
     """On version 2's grid with K % 32 == 0 both run 32-deep k-tiles in the
     same order, with the same tiles and split: bitwise equal."""
-    for m, n, k in [(256, 256, 64), (512, 768, 320), (256, 512, 32), (512, 512, 512), (256, 256, 1024)]:
+    for m, n, k in [(256, 256, 64), (512, 768, 320), (256, 512, 32), (512, 512, 512), (256, 256, 1024),
+                    (2304, 2048, 2048)]:
         A, B = make_inputs(m, n, k, "normal", seed=m + k, dtype=np.float32)
         assert np.array_equal(_run(A, B, 2).view(np.uint32), _run(A, B, 3).view(np.uint32))
 

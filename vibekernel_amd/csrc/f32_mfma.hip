@@ -331,7 +331,9 @@ extern "C" int vk_timeline_f32_read(unsigned long long* host, int waves) {
 //    costs the matrix cores next to nothing (measured at 4096^3, 2 rounds on
 //    one box: 943.8 / 945.3 us per launch against 939.9 / 941.7 with
 //    256x256 tiles; 4096 x 4352 x 4096 1188 / 1193 against 1873 / 1861;
-//    6144 x 4096 x 4096 1416 / 1417 against 1900 / 1881).
+//    6144 x 4096 x 4096 1416 / 1417 against 1900 / 1881); with a part-empty
+//    last round split (below): 4096 x 4352 x 4096 1063, 3072^3 430.5
+//    against 535.6, 2304 x 2048 x 2048 168.4 against 237.1.
 // A wave's fragments are read one group of 4 steps ahead into a second
 // register set: the next group's kReads reads (kNB A reads of 16 bytes, 2 kNB
 // pairs of B values) one after each of the first kReads MFMAs from the
@@ -362,10 +364,12 @@ struct F32W4 {
   static_assert(kReads <= 3 * kNB * kNB, "a group's reads fit its last three steps");
 };
 
-// ---- split K (kNB = 2) for grids whose 128x128 tiles fill at most half of
-// the CUs: sk_plan_fill's pieces (at least kF32MinIters k-tiles each, the
-// last one k-tile longer), the pieces of a tile meeting as in the fp16
-// 128x128 kernel: per (tile, wave) an arrival counter; a finishing wave that
+// ---- split K (kNB = 2): for grids whose 128x128 tiles fill at most half of
+// the CUs, sk_plan_fill's pieces of every tile (at least kF32MinIters
+// k-tiles each, the last one k-tile longer); otherwise sk_plan's split tail
+// (the tiles of a part-empty last round of the CUs cut into k-slices, the
+// others whole, as the fp16 version 9).  The pieces of a tile meet as in
+// the fp16 128x128 kernel: per (tile, wave) an arrival counter; a finishing wave that
 // finds every other piece in memory is the last and writes nothing,
 // otherwise it writes its 16 KB fp32 partial with sc1 stores, waits for them
 // and increments the counter, and the one that sees np - 1 is the last.  The
@@ -389,8 +393,13 @@ inline bool f32_small_tiles(size_t m, size_t n, int num_cus) {
   return 4 * ((f32_tiles(m, n, 256) + c - 1) / c) > (f32_tiles(m, n, 128) + c - 1) / c;
 }
 inline SkPlan f32_plan(size_t m, size_t n, size_t k, int num_cus) {
-  return sk_plan_fill(f32_tiles(m, n, 128), (int64_t)((k + 31) / 32), num_cus, kF32MinIters);
+  const int64_t T = f32_tiles(m, n, 128), I = (int64_t)((k + 31) / 32);
+  const SkPlan fill = sk_plan_fill(T, I, num_cus, kF32MinIters);
+  return fill.units > 0 ? fill : sk_plan(T, I, num_cus);
 }
+// Extra k-tiles of a split tile's last piece: one in a fill plan (no whole
+// tiles), sk_plan's own number in a tail plan.
+inline int f32_last_extra(const SkPlan& p) { return p.dp > 0 ? kSkLastExtra : kFillLastExtra; }
 
 // Vector v of a wave's accumulators: block (v / 4kNB, (v / 4) % kNB),
 // registers 4 (v % 4) .. + 3.  In a partial, vector v of every lane sits at
@@ -482,8 +491,9 @@ __device__ __forceinline__ void f32_split_sum(float16v_ (&acc)[kNB][kNB], int np
   }
 }
 
-// kSplit: this workgroup is unit blockIdx.x of the split plan {0, units,
-// pieces, chunks}; part and counters are the workspace.  kKMask (with kEdge,
+// kSplit: this workgroup is number blockIdx.x of the split plan {dp, units,
+// pieces, chunks} (the last piece of a split tile `extra` k-tiles longer);
+// part and counters are the workspace.  kKMask (with kEdge,
 // for K % 32 != 0): the last k-tile reaches past K.  B's k-rows past K read
 // zeros (the buffer range); A's k past K in memory are the next row's
 // values, which must not meet those zeros (an infinity would make a NaN), so
@@ -492,9 +502,9 @@ __device__ __forceinline__ void f32_split_sum(float16v_ (&acc)[kNB][kNB], int np
 // side).
 template <int kNB, bool kEdge, bool kSplit, bool kKMask = false>
 __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict__ A, const float* __restrict__ B,
-                                                        float* __restrict__ C, int M, int N, int K, int units,
-                                                        int pieces, int chunks, float* __restrict__ part,
-                                                        unsigned* __restrict__ counters) {
+                                                        float* __restrict__ C, int M, int N, int K, int dp,
+                                                        int units, int pieces, int chunks, int extra,
+                                                        float* __restrict__ part, unsigned* __restrict__ counters) {
   using W = F32W4<kNB>;
   constexpr int BK = W::BK, kT = W::kT, kQ = W::kQ;
   constexpr int kDA = W::kDA, kDB = W::kDB, kD = W::kD;
@@ -509,7 +519,7 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
   int tm, tn, kb = 0, nk = iters;
   SkWork w{};
   if constexpr (kSplit) {
-    w = sk_work(blockIdx.x, tiles_m * tiles_n, iters, SkPlan{0, units, pieces, chunks}, kFillLastExtra);
+    w = sk_work(blockIdx.x, tiles_m * tiles_n, iters, SkPlan{dp, units, pieces, chunks}, extra);
     raster_tile(w.cid, tiles_m, tiles_n, tm, tn);
     kb = w.kb;
     nk = w.ke - w.kb;
@@ -728,10 +738,11 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
 
   const int lane_e = (int)__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
   unsigned* cnt = nullptr;
-  if constexpr (kSplit) {
+  const bool split = kSplit && w.np > 1;  // whole tiles of a tail plan store at once
+  if (split) {
     const __amdgpu_buffer_rsrc_t prsrc =
         __builtin_amdgcn_make_buffer_rsrc(part, 0, (int)((size_t)units * kF32SlotBytes), kBufferWord3);
-    const SkPlan plan{0, units, pieces, chunks};
+    const SkPlan plan{dp, units, pieces, chunks};
     const int T = tiles_m * tiles_n;
     auto part_off = [&](int q) {
       return (uint32_t)((size_t)sk_unit_of(plan, T, w.tile, q) * kF32SlotBytes) + (uint32_t)wave * kF32WaveBytes;
@@ -751,9 +762,7 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
         const int col = col0 + bj * 32 + (lane_e & 31);
         if (!kEdge || (row < M && col < N)) C[(size_t)row * N + col] = acc[bi][bj][r];
       }
-  if constexpr (kSplit) {
-    if (lane_e == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
+  if (split && lane_e == 0) __hip_atomic_store(cnt, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #if VK_TIMELINE
   wait_vmcnt0_ordered();
   const unsigned long long tl_exit = __builtin_amdgcn_s_memrealtime();
@@ -785,10 +794,10 @@ hipError_t launch_w4(const GemmArgs& a, const SkPlan& p) {
       if (e != hipSuccess) return e;
     }
   }
-  const int grid = kSplit ? p.units : (int)f32_tiles(a.m, a.n, W::kT);
+  const int grid = kSplit ? p.dp + p.units : (int)f32_tiles(a.m, a.n, W::kT);
   hipLaunchKernelGGL(kfn, dim3(grid), dim3(256), W::kLdsBytes, a.stream, static_cast<const float*>(a.A),
-                     static_cast<const float*>(a.B), static_cast<float*>(a.C), (int)a.m, (int)a.n, (int)a.k, p.units,
-                     p.pieces, p.chunks, part, counters);
+                     static_cast<const float*>(a.B), static_cast<float*>(a.C), (int)a.m, (int)a.n, (int)a.k, p.dp,
+                     p.units, p.pieces, p.chunks, f32_last_extra(p), part, counters);
   return hipGetLastError();
 }
 
