@@ -125,30 +125,31 @@ def test_edge_split_plan_follows_shape():
 
 def test_f32_split_workspace_follows_shape():
     """fp32 versions 2 and 3 take 128 x 128 tiles unless 256 x 256 ones fill
-    the CUs in as few rounds, and split K (pieces of at least 2 k-tiles of
-    32) where the 128 x 128 tiles fill at most half of the CUs, or the tiles
-    of a part-empty last round where version 9's schedule does: the 8 KB
-    counter block plus one 64 KB partial slot per piece (256 CUs assumed)."""
+    the CUs in as few rounds, 64 x 64 tiles where the 128 x 128 ones fill at
+    most half of the CUs, and split K (pieces of at least 2 k-tiles of 32)
+    where the chosen tiles fill at most half of the CUs, or the tiles of a
+    part-empty last round where version 9's schedule does: the 8 KB counter
+    block plus one partial slot (the tile in fp32: 64 or 16 KB) per piece
+    (256 CUs assumed)."""
     from vibekernel_amd import _abi
     f32 = _abi.DTYPE_F32
     for v in (2, 3):
         assert _abi.query(v, f32).uses_workspace == 1
         assert _abi.workspace_bytes(v, f32, 4096, 4096, 4096) == 0   # 256 tiles of 256 x 256
         assert _abi.workspace_bytes(v, f32, 2048, 2048, 2048) == 0   # 256 tiles of 128 x 128: whole
-        assert _abi.workspace_bytes(v, f32, 1024, 1024, 1024) == 8192 + 256 * 65536  # 64 tiles x 4 pieces
-        assert _abi.workspace_bytes(v, f32, 512, 512, 512) == 8192 + 128 * 65536     # 16 tiles x 8 pieces
-        assert _abi.workspace_bytes(v, f32, 1280, 1280, 256) == 8192 + 200 * 65536   # 100 tiles x 2 pieces
+        assert _abi.workspace_bytes(v, f32, 1024, 1024, 1024) == 0   # 256 tiles of 64 x 64: whole
+        assert _abi.workspace_bytes(v, f32, 512, 512, 512) == 8192 + 256 * 16384      # 64 x 64: 64 tiles x 4 pieces
+        assert _abi.workspace_bytes(v, f32, 256, 256, 1024) == 8192 + 128 * 16384     # 16 tiles x 8 pieces
         assert _abi.workspace_bytes(v, f32, 4096, 4352, 4096) == 8192 + 256 * 65536  # 1088 tiles: 64 in the tail x 4
         assert _abi.workspace_bytes(v, f32, 2304, 2048, 2048) == 8192 + 128 * 65536  # 288 tiles: 32 in the tail x 4
         assert _abi.workspace_bytes(v, f32, 2304, 2304, 2048) == 8192 + 204 * 65536  # 324 tiles: 68 in the tail x 3
         assert _abi.workspace_bytes(v, f32, 2304, 2048, 1024) == 0   # 32 k-tiles: the tail left whole
         assert _abi.workspace_bytes(v, f32, 256, 256, 32) == 0       # one k-tile
-        assert _abi.workspace_bytes(v, f32, 256, 256, 1024) == 8192 + 32 * 65536     # 4 tiles x 8 pieces
         assert _abi.workspace_bytes(v, f32, 4096, 4096, 1040) == 0   # 256 tiles of 256 x 256 (eight-wave kernel)
-        assert _abi.workspace_bytes(v, f32, 1024, 1024, 1040) == 8192 + 256 * 65536  # 33 k-tiles, the last masked
-    assert _abi.workspace_bytes(3, f32, 1000, 1000, 1024) == 8192 + 256 * 65536  # 64 edge tiles x 4 pieces
+        assert _abi.workspace_bytes(v, f32, 512, 512, 1040) == 8192 + 256 * 16384     # 33 k-tiles, the last masked
+    assert _abi.workspace_bytes(3, f32, 1000, 1000, 1024) == 0       # 256 edge tiles of 64 x 64
     assert _abi.workspace_bytes(3, f32, 300, 260, 96) == 0           # 3 k-tiles: too shallow to split
-    assert _abi.workspace_bytes(3, f32, 300, 260, 128) == 8192 + 18 * 65536     # 9 tiles x 2 pieces
+    assert _abi.workspace_bytes(3, f32, 300, 260, 128) == 8192 + 50 * 16384      # 25 tiles x 2 pieces
 
 
 def test_single_hip_runtime_in_process():

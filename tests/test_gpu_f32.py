@@ -5,13 +5,15 @@
   64 x 64 where those fill the CUs in fewer rounds): equal to the oracle,
   bit for bit, on every shape;
 * version 2 (matrix cores, v_mfma_f32_32x32x2_f32, two products per step;
-  the four-wave kernel when K % 32 == 0 -- 256 x 256 tiles where they give
-  every CU one, else 128 x 128 tiles, K split over idle CUs where those fill
-  at most half of them; K % 32 == 16 on 256 x 256 tiles: the eight-wave
-  kernel with 16-deep k-tiles): integer inputs exact; random inputs within 2 k u |A||B| of
-  the exact (fp64) product; bitwise repeatable launch to launch (a split
-  shape); shapes include one k-tile (K = 32), more tiles than CUs, 128 x 128
-  tiles whole and split into 2 to 8 pieces;
+  the four-wave kernel when K % 32 == 0 -- 256 x 256 tiles where they fill
+  the CUs in as few rounds as smaller ones, else 128 x 128 tiles, or 64 x 64
+  where those fill at most half of the CUs, K split where the tiles fill at
+  most half of them or leave a last round part empty; K % 32 == 16 on
+  256 x 256 tiles: the eight-wave kernel with 16-deep k-tiles): integer
+  inputs exact; random inputs within 2 k u |A||B| of the exact (fp64)
+  product; bitwise repeatable launch to launch (a split shape); shapes
+  include one k-tile (K = 32), more tiles than CUs, every tile size whole
+  and split;
 * version 3 (version 2 with masked edges: any M, N and K multiples of 4; the
   four-wave kernel when K % 32 == 0 or on 128 x 128 tiles, the last k-tile
   then masked per lane): the same bars on ragged shapes,
@@ -32,22 +34,22 @@ SHAPES_V1 = [(128, 128, 16), (256, 384, 64), (512, 512, 512), (1, 1, 1), (17, 33
              (128, 256, 16), (256, 512, 32), (384, 768, 48), (1024, 512, 1024), (128, 256, 2000),
              (4000, 4000, 40), (4096, 4096, 32)]
 # (version 2, 256 CUs) 256 x 256 tiles: (4096, 4096, 64); 128 x 128 whole:
-# (512, 256, 64), (256, 256, 32), (2048, 2048, 128), (4352, 4096, 64) (272
-# tiles of 256 x 256 would take two rounds of the CUs); split: (1280, 1280,
-# 256) in 2 pieces, (768, 512, 256), (1024, 1024, 512) and (1024, 1024,
-# 1024) in 4, (512, 512, 512) and (256, 256, 1024) in 8
+# (2048, 2048, 128), (4352, 4096, 64) (272 tiles of 256 x 256 would take two
+# rounds of the CUs); 128 x 128 with 256 whole tiles and a tail split:
+# (2304, 2048, 2048) 32 tail tiles in 4 pieces, (2304, 2304, 2048) 68 in 3
+# (one chunk); 64 x 64 whole: (512, 256, 64), (256, 256, 32), (1024, 1024,
+# 512), (1024, 1024, 1024), (1280, 1280, 256); 64 x 64 split: (768, 512,
+# 256) in 2 pieces, (512, 512, 512) in 4, (256, 256, 1024) in 8;
 # 4096 x 4096 x 48: the eight-wave kernel; (256, 256, 16), (256, 512, 48):
-# 128 x 128 tiles with the last k-tile masked; (2304, 2048, 2048): 256 whole
-# tiles and 32 in a tail split in 4; (2304, 2304, 2048): 68 in a tail split
-# in 3, one chunk
+# 64 x 64 tiles with the last k-tile masked
 SHAPES_V2 = [(256, 256, 16), (512, 256, 64), (256, 512, 48), (768, 512, 256), (1024, 1024, 512), (256, 256, 32),
              (4352, 4096, 64), (512, 512, 512), (1024, 1024, 1024), (256, 256, 1024), (2048, 2048, 128),
              (4096, 4096, 64), (1280, 1280, 256), (4096, 4096, 48), (2304, 2048, 2048),
              (2304, 2304, 2048)]
-# split edge tiles: (1000, 1000, 1024) in 4 pieces, (300, 600, 2048) and
-# (129, 4, 512) in 8; the k mask on 128 x 128 tiles: (1000, 1000, 1000) in
-# 4 pieces, (300, 260, 100) in 2, (17, 36, 68) whole; 4096 x 4096 x 100: the
-# eight-wave kernel with its mask; (2100, 2000, 2048): a split tail
+# 64 x 64 edge tiles split: (300, 600, 2048) in 5 pieces, (129, 4, 512) in
+# 8; the k mask on 64 x 64 tiles: (300, 260, 100) in 2 pieces, (1000, 1000,
+# 1000) and (17, 36, 68) whole; 4096 x 4096 x 100: the eight-wave kernel with
+# its mask; (2100, 2000, 2048): 128 x 128 edge tiles with a split tail
 SHAPES_V3 = [(1, 4, 4), (17, 36, 68), (300, 260, 100), (257, 512, 36), (1000, 1000, 1000), (256, 256, 64),
              (300, 260, 96), (257, 516, 64), (1000, 1000, 1024), (1, 4, 32), (300, 600, 2048), (129, 4, 512),
              (4096, 4096, 100), (2100, 2000, 2048)]
@@ -113,11 +115,11 @@ def test_f32_4096(gpu, oracle, version):
 
 def test_f32_mfma_repeat_deterministic(gpu):
     """20 launches of version 2 with C poisoned before each: bitwise equal
-    (48 tiles of 128 x 128, K split in 5: whichever piece arrives last, the
+    (64 tiles of 64 x 64, K split in 4: whichever piece arrives last, the
     pieces are summed in k order)."""
     import torch
     import vibekernel_amd as vk
-    m, n, k = 1024, 768, 512
+    m, n, k = 512, 512, 1024
     g = torch.Generator(device="cuda:0").manual_seed(2)
     A = torch.rand((m, k), generator=g, device="cuda:0") * 2 - 1
     B = torch.rand((k, n), generator=g, device="cuda:0") * 2 - 1

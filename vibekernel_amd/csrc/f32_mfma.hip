@@ -334,6 +334,13 @@ extern "C" int vk_timeline_f32_read(unsigned long long* host, int waves) {
 //    6144 x 4096 x 4096 1416 / 1417 against 1900 / 1881); with a part-empty
 //    last round split (below): 4096 x 4352 x 4096 1063, 3072^3 430.5
 //    against 535.6, 2304 x 2048 x 2048 168.4 against 237.1.
+//  * kNB = 1, 64x64 tiles (one 32x32 block per wave, 16 accumulators) where
+//    the 128x128 tiles fill at most half of the CUs: per k-tile 16 MFMAs of
+//    the one block, 3 fragment reads per group and 4 loads per wave.
+//    Measured against 128x128 tiles (2 rounds, one box, us per launch):
+//    512^3 9.35 against 15.75, 1024^3 20.4 / 25.9, 1024 x 1024 x 512 11.5 /
+//    17.9, 768 x 512 x 256 6.8 / 12.5, v3 1000^3 22.5 / 27.2, 1280^3 42.3 /
+//    48.5.
 // A wave's fragments are read one group of 4 steps ahead into a second
 // register set: the next group's kReads reads (kNB A reads of 16 bytes, 2 kNB
 // pairs of B values) one after each of the first kReads MFMAs from the
@@ -359,8 +366,16 @@ struct F32W4 {
   static constexpr int kDB = BK / kBRowsPerDma / 4;      // B loads per wave per k-tile
   static constexpr int kD = kDA + kDB;
   static constexpr int kReads = 3 * kNB;                 // fragment reads per group of 4 steps
-  static constexpr int kLoadEvery = 3 * kNB * kNB / kD;  // MFMAs per load in the last 3 steps
-  static_assert(kLdsBytes <= 160 * 1024 && kLoadEvery >= 1 && kD * kLoadEvery <= 3 * kNB * kNB, "schedule");
+  // MFMAs per load in the last 3 steps; 0 (64x64 tiles: 4 loads, 3 MFMAs):
+  // load m after MFMA m, the last two after the last MFMA
+  static constexpr int kLoadEvery = 3 * kNB * kNB / kD;
+  static_assert(kLdsBytes <= 160 * 1024 && (kLoadEvery >= 1 || kNB == 1) && kD * kLoadEvery <= 3 * kNB * kNB,
+                "schedule");
+  // loads [load_begin(m), load_begin(m + 1)) go out after MFMA m of the last 3 steps
+  static constexpr int load_begin(int m) {
+    return kLoadEvery >= 1 ? (m + kLoadEvery - 1) / kLoadEvery < kD ? (m + kLoadEvery - 1) / kLoadEvery : kD
+                           : m < 3 * kNB * kNB ? m : kD;
+  }
   static_assert(kReads <= 3 * kNB * kNB, "a group's reads fit its last three steps");
 };
 
@@ -380,8 +395,9 @@ struct F32W4 {
 // 15.5 against 16.7, 512 x 512 x 256 12.8 against 15.0, 256 x 512 x 512
 // 15.2 against 16.6.
 constexpr int kF32MinIters = 2;
-constexpr size_t kF32SlotBytes = (size_t)128 * 128 * sizeof(float);  // one tile's fp32 partial
-constexpr uint32_t kF32WaveBytes = 64 * 64 * sizeof(float);          // a wave's 64x64 quarter
+// One tile's fp32 partial, and a wave's quarter of it.
+constexpr size_t f32_slot_bytes(int nb) { return (size_t)(64 * nb) * (64 * nb) * sizeof(float); }
+constexpr uint32_t f32_wave_bytes(int nb) { return (uint32_t)(32 * nb) * (32 * nb) * sizeof(float); }
 
 __host__ __device__ inline int64_t f32_tiles(size_t m, size_t n, size_t t) {
   return (int64_t)((m + t - 1) / t) * (int64_t)((n + t - 1) / t);
@@ -392,8 +408,13 @@ inline bool f32_small_tiles(size_t m, size_t n, int num_cus) {
   const int64_t c = num_cus > 0 ? num_cus : 1;
   return 4 * ((f32_tiles(m, n, 256) + c - 1) / c) > (f32_tiles(m, n, 128) + c - 1) / c;
 }
-inline SkPlan f32_plan(size_t m, size_t n, size_t k, int num_cus) {
-  const int64_t T = f32_tiles(m, n, 128), I = (int64_t)((k + 31) / 32);
+// Blocks of 32x32 per wave side off the 256x256 tiles: 2 (128x128 tiles), or
+// 1 (64x64) where the 128x128 tiles fill at most half of the CUs.
+inline int f32_small_nb(size_t m, size_t n, int num_cus) {
+  return 2 * f32_tiles(m, n, 128) <= (num_cus > 0 ? num_cus : 1) ? 1 : 2;
+}
+inline SkPlan f32_plan(size_t m, size_t n, size_t k, int num_cus, int nb) {
+  const int64_t T = f32_tiles(m, n, 64 * (size_t)nb), I = (int64_t)((k + 31) / 32);
   const SkPlan fill = sk_plan_fill(T, I, num_cus, kF32MinIters);
   return fill.units > 0 ? fill : sk_plan(T, I, num_cus);
 }
@@ -440,7 +461,7 @@ template <int kNB, int NP, typename PartOff>
 __device__ __forceinline__ void f32_split_sum_n(float16v_ (&acc)[kNB][kNB], int p, int lane,
                                                 __amdgpu_buffer_rsrc_t part, PartOff part_off) {
   constexpr int kV = 4 * kNB * kNB;
-  constexpr int kB = NP <= 4 ? 8 : 4;
+  constexpr int kB = (NP <= 4 ? 8 : 4) < kV ? (NP <= 4 ? 8 : 4) : kV;
   static_assert(kV % kB == 0, "whole batches");
 #pragma unroll
   for (int v0 = 0; v0 < kV; v0 += kB) {
@@ -508,8 +529,8 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
   using W = F32W4<kNB>;
   constexpr int BK = W::BK, kT = W::kT, kQ = W::kQ;
   constexpr int kDA = W::kDA, kDB = W::kDB, kD = W::kD;
-  static_assert(!kSplit || kNB == 2, "K is split on the 128x128 tiles only");
-  static_assert(!kKMask || (kEdge && kNB == 2), "the k mask is for the 128x128 edge tiles");
+  static_assert(!kSplit || kNB <= 2, "K is split on the 128x128 and 64x64 tiles only");
+  static_assert(!kKMask || (kEdge && kNB <= 2), "the k mask is for the 128x128 and 64x64 edge tiles");
   extern __shared__ __attribute__((aligned(1024))) char lds[];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -721,8 +742,8 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
                 __builtin_amdgcn_sched_barrier(0);
                 read_one(f[0], s_next, 0, m);
               }
-              if (m % W::kLoadEvery == 0 && m / W::kLoadEvery < kD) {
-                const int d = m / W::kLoadEvery;
+#pragma unroll
+              for (int d = W::load_begin(m); d < W::load_begin(m + 1); d++) {
                 __builtin_amdgcn_sched_barrier(0);
                 issue_one(kt_next, t & 1, (d & 1) ? kDA + (d >> 1) : (d >> 1));
               }
@@ -741,11 +762,12 @@ __global__ __launch_bounds__(256) void f32_mfma4_kernel(const float* __restrict_
   const bool split = kSplit && w.np > 1;  // whole tiles of a tail plan store at once
   if (split) {
     const __amdgpu_buffer_rsrc_t prsrc =
-        __builtin_amdgcn_make_buffer_rsrc(part, 0, (int)((size_t)units * kF32SlotBytes), kBufferWord3);
+        __builtin_amdgcn_make_buffer_rsrc(part, 0, (int)((size_t)units * f32_slot_bytes(kNB)), kBufferWord3);
     const SkPlan plan{dp, units, pieces, chunks};
     const int T = tiles_m * tiles_n;
     auto part_off = [&](int q) {
-      return (uint32_t)((size_t)sk_unit_of(plan, T, w.tile, q) * kF32SlotBytes) + (uint32_t)wave * kF32WaveBytes;
+      return (uint32_t)((size_t)sk_unit_of(plan, T, w.tile, q) * f32_slot_bytes(kNB)) +
+             (uint32_t)wave * f32_wave_bytes(kNB);
     };
     cnt = counters + (size_t)w.tile * kSkWaves + wave;
     if (!f32_split_arrive(acc, w.np, w.p, lane_e, prsrc, part_off, cnt)) return;
@@ -803,23 +825,29 @@ hipError_t launch_w4(const GemmArgs& a, const SkPlan& p) {
 
 bool f32_mfma_edge_shape_ok(size_t m, size_t n, size_t k);
 
-// The 128x128 tiles (f32_small_tiles), K split where they fill at most half
-// of the CUs; K % 32 != 0 through the edge kernel with the k mask (also on
+// The 128x128 or 64x64 tiles (f32_small_tiles, f32_small_nb), K split
+// where they fill at most half of the CUs or leave the last round part
+// empty; K % 32 != 0 through the edge kernel with the k mask (also on
 // version 2's grid, whose 16-deep eight-wave kernel has 256x256 tiles only;
 // the caller checks the edge kernel's size limits).
+template <int kNB, bool kEdge>
+hipError_t launch_f32_small_nb(const GemmArgs& a) {
+  const SkPlan p = f32_plan(a.m, a.n, a.k, a.num_cus, kNB);
+  if (a.k % 32 != 0)
+    return p.units > 0 ? launch_w4<kNB, true, true, true>(a, p) : launch_w4<kNB, true, false, true>(a, p);
+  return p.units > 0 ? launch_w4<kNB, kEdge, true>(a, p) : launch_w4<kNB, kEdge, false>(a, p);
+}
 template <bool kEdge>
 hipError_t launch_f32_small(const GemmArgs& a) {
-  const SkPlan p = f32_plan(a.m, a.n, a.k, a.num_cus);
-  if (a.k % 32 != 0)
-    return p.units > 0 ? launch_w4<2, true, true, true>(a, p) : launch_w4<2, true, false, true>(a, p);
-  return p.units > 0 ? launch_w4<2, kEdge, true>(a, p) : launch_w4<2, kEdge, false>(a, p);
+  return f32_small_nb(a.m, a.n, a.num_cus) == 1 ? launch_f32_small_nb<1, kEdge>(a) : launch_f32_small_nb<2, kEdge>(a);
 }
 
 // Workspace of versions 2 and 3: the split's counters and partials.
 size_t f32_workspace(size_t m, size_t n, size_t k, int num_cus) {
   if (!f32_small_tiles(m, n, num_cus) || (k % 32 != 0 && !f32_mfma_edge_shape_ok(m, n, k))) return 0;
-  const SkPlan p = f32_plan(m, n, k, num_cus);
-  return p.units > 0 ? kSkCounterBytes + (size_t)p.units * kF32SlotBytes : 0;
+  const int nb = f32_small_nb(m, n, num_cus);
+  const SkPlan p = f32_plan(m, n, k, num_cus, nb);
+  return p.units > 0 ? kSkCounterBytes + (size_t)p.units * f32_slot_bytes(nb) : 0;
 }
 
 // 32-deep k-tiles when K allows (one barrier per 128 MFMAs of a wave:
