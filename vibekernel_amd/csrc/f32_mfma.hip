@@ -22,13 +22,15 @@
 //    register r holds D[8*(r/4) + 4*(l/32) + r%4][l%32] of the block;
 //  * per element the sum runs over the steps in ascending order, k-tile by
 //    k-tile, so the two kernels give the same bits.
-// Versions 2 and 3 with K % 32 == 0 run the four-wave kernel
-// (f32_mfma4_kernel: one wave per SIMD owning a 128x128 quarter, 32-deep
-// k-tiles in 2 stages of 64 KB; for version 3 with buffer loads and bounded
-// stores); other K run the eight-wave kernel (f32_mfma_kernel: wave w owns
-// rows 128*(w/4) and columns 64*(w%4) onward, 4x2 blocks of 32x32; version
-// 2 with K % 32 == 16: BK = 16 in 4 stages of 32 KB; version 3: BK = 32 in
-// 2 stages, the last k-tile masked per lane).  Interleaved on one box, the
+// Versions 2 and 3 on 256x256 tiles with K % 32 == 0 run the four-wave
+// kernel (f32_mfma4_kernel: one wave per SIMD owning a 128x128 quarter,
+// 32-deep k-tiles in 2 stages of 64 KB; for version 3 with buffer loads and
+// bounded stores); other K on 256x256 tiles run the eight-wave kernel
+// (f32_mfma_kernel: wave w owns rows 128*(w/4) and columns 64*(w%4) onward,
+// 4x2 blocks of 32x32; version 2 with K % 32 == 16: BK = 16 in 4 stages of
+// 32 KB; version 3: BK = 32 in 2 stages, the last k-tile masked per lane).
+// Grids of few 256x256 tiles take the four-wave kernel on 128x128 or 64x64
+// tiles for any K (below).  Interleaved on one box, the
 // four-wave form measured 0.8-1.4 % faster at 4096^3 (0.8 % at 4096 x 4096
 // x 8192) and with edges 1.1 % at 4000^3 and 0.7 % at 1000 x 3000 x 2048;
 // with the last k-tile's per-lane masking as well (64-bit mask shifts
