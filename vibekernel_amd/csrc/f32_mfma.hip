@@ -457,13 +457,16 @@ __device__ __forceinline__ bool f32_split_arrive(const float16v_ (&acc)[kNB][kNB
 
 // The last arrival: acc <- P0 + P1 + ... + P(NP-1), left to right, with
 // P(p) = acc.  Every piece's vectors are loaded kB at a time (NP x kB loads
-// in flight, at most 128 registers), the own piece's slot too (not used; it
-// always lies inside the workspace, so no branch is needed).
+// in flight, at most 64 registers, which keeps the 128x128 split instance at
+// 216 registers: two workgroups per CU, where batches of twice the size
+// needed 288 -- measured 3072^3 411.1 against 431.7 us, 2304 x 2048 x 2048
+// 160.7 against 168.3), the own piece's slot too (not used; it always lies
+// inside the workspace, so no branch is needed).
 template <int kNB, int NP, typename PartOff>
 __device__ __forceinline__ void f32_split_sum_n(float16v_ (&acc)[kNB][kNB], int p, int lane,
                                                 __amdgpu_buffer_rsrc_t part, PartOff part_off) {
   constexpr int kV = 4 * kNB * kNB;
-  constexpr int kB = (NP <= 4 ? 8 : 4) < kV ? (NP <= 4 ? 8 : 4) : kV;
+  constexpr int kB = (NP <= 4 ? 4 : 2) < kV ? (NP <= 4 ? 4 : 2) : kV;
   static_assert(kV % kB == 0, "whole batches");
 #pragma unroll
   for (int v0 = 0; v0 < kV; v0 += kB) {
