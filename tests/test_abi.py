@@ -125,8 +125,8 @@ def test_edge_split_plan_follows_shape():
 
 def test_f32_split_workspace_follows_shape():
     """fp32 versions 2 and 3 take 128 x 128 tiles unless 256 x 256 ones fill
-    the CUs in as few rounds, 64 x 64 tiles where the 128 x 128 ones fill at
-    most half of the CUs, and split K (pieces of at least 2 k-tiles of 32)
+    the CUs in as few rounds, 64 x 64 tiles where the 128 x 128 ones are
+    fewer than the CUs, and split K (pieces of at least 2 k-tiles of 32)
     where the chosen tiles fill at most half of the CUs, or the tiles of a
     part-empty last round where version 9's schedule does: the 8 KB counter
     block plus one partial slot (the tile in fp32: 64 or 16 KB) per piece
@@ -138,6 +138,7 @@ def test_f32_split_workspace_follows_shape():
         assert _abi.workspace_bytes(v, f32, 4096, 4096, 4096) == 0   # 256 tiles of 256 x 256
         assert _abi.workspace_bytes(v, f32, 2048, 2048, 2048) == 0   # 256 tiles of 128 x 128: whole
         assert _abi.workspace_bytes(v, f32, 1024, 1024, 1024) == 0   # 256 tiles of 64 x 64: whole
+        assert _abi.workspace_bytes(v, f32, 1536, 1536, 1536) == 8192 + 192 * 16384  # 576 tiles of 64 x 64: 64 in the tail x 3
         assert _abi.workspace_bytes(v, f32, 512, 512, 512) == 8192 + 256 * 16384      # 64 x 64: 64 tiles x 4 pieces
         assert _abi.workspace_bytes(v, f32, 256, 256, 1024) == 8192 + 128 * 16384     # 16 tiles x 8 pieces
         assert _abi.workspace_bytes(v, f32, 4096, 4352, 4096) == 8192 + 256 * 65536  # 1088 tiles: 64 in the tail x 4

@@ -7,7 +7,7 @@
 * version 2 (matrix cores, v_mfma_f32_32x32x2_f32, two products per step;
   the four-wave kernel when K % 32 == 0 -- 256 x 256 tiles where they fill
   the CUs in as few rounds as smaller ones, else 128 x 128 tiles, or 64 x 64
-  where those fill at most half of the CUs, K split where the tiles fill at
+  where those are fewer than the CUs, K split where the tiles fill at
   most half of them or leave a last round part empty; K % 32 == 16 on
   256 x 256 tiles: the eight-wave kernel with 16-deep k-tiles): integer
   inputs exact; random inputs within 2 k u |A||B| of the exact (fp64)
@@ -41,11 +41,12 @@ SHAPES_V1 = [(128, 128, 16), (256, 384, 64), (512, 512, 512), (1, 1, 1), (17, 33
 # 512), (1024, 1024, 1024), (1280, 1280, 256); 64 x 64 split: (768, 512,
 # 256) in 2 pieces, (512, 512, 512) in 4, (256, 256, 1024) in 8;
 # 4096 x 4096 x 48: the eight-wave kernel; (256, 256, 16), (256, 512, 48):
-# 64 x 64 tiles with the last k-tile masked
+# 64 x 64 tiles with the last k-tile masked; (1536, 1536, 1536): 576 tiles of
+# 64 x 64, 64 of them in a tail split in 3
 SHAPES_V2 = [(256, 256, 16), (512, 256, 64), (256, 512, 48), (768, 512, 256), (1024, 1024, 512), (256, 256, 32),
              (4352, 4096, 64), (512, 512, 512), (1024, 1024, 1024), (256, 256, 1024), (2048, 2048, 128),
              (4096, 4096, 64), (1280, 1280, 256), (4096, 4096, 48), (2304, 2048, 2048),
-             (2304, 2304, 2048)]
+             (2304, 2304, 2048), (1536, 1536, 1536)]
 # 64 x 64 edge tiles split: (300, 600, 2048) in 5 pieces, (129, 4, 512) in
 # 8; the k mask on 64 x 64 tiles: (300, 260, 100) in 2 pieces, (1000, 1000,
 # 1000) and (17, 36, 68) whole; 4096 x 4096 x 100: the eight-wave kernel with

@@ -337,7 +337,7 @@ extern "C" int vk_timeline_f32_read(unsigned long long* host, int waves) {
 //    last round split (below): 4096 x 4352 x 4096 1063, 3072^3 430.5
 //    against 535.6, 2304 x 2048 x 2048 168.4 against 237.1.
 //  * kNB = 1, 64x64 tiles (one 32x32 block per wave, 16 accumulators) where
-//    the 128x128 tiles fill at most half of the CUs: per k-tile 16 MFMAs of
+//    the 128x128 tiles are fewer than the CUs: per k-tile 16 MFMAs of
 //    the one block, 3 fragment reads per group and 4 loads per wave.
 //    Measured against 128x128 tiles (2 rounds, one box, us per launch):
 //    512^3 9.35 against 15.75, 1024^3 20.4 / 25.9, 1024 x 1024 x 512 11.5 /
@@ -411,9 +411,13 @@ inline bool f32_small_tiles(size_t m, size_t n, int num_cus) {
   return 4 * ((f32_tiles(m, n, 256) + c - 1) / c) > (f32_tiles(m, n, 128) + c - 1) / c;
 }
 // Blocks of 32x32 per wave side off the 256x256 tiles: 2 (128x128 tiles), or
-// 1 (64x64) where the 128x128 tiles fill at most half of the CUs.
+// 1 (64x64) where the 128x128 tiles are fewer than the CUs (several 64x64
+// workgroups share a CU: 32 KB of LDS and at most 136 registers each).
+// Measured against 128x128 tiles (2 rounds, one box, us per launch): 1536^3
+// (144 tiles of 128x128) 58.6 against 96.3; where the 128x128 tiles fill
+// whole rounds they win: 3072^3 409 against 452, 2048^3 128 / 126.
 inline int f32_small_nb(size_t m, size_t n, int num_cus) {
-  return 2 * f32_tiles(m, n, 128) <= (num_cus > 0 ? num_cus : 1) ? 1 : 2;
+  return f32_tiles(m, n, 128) < (num_cus > 0 ? num_cus : 1) ? 1 : 2;
 }
 inline SkPlan f32_plan(size_t m, size_t n, size_t k, int num_cus, int nb) {
   const int64_t T = f32_tiles(m, n, 64 * (size_t)nb), I = (int64_t)((k + 31) / 32);
