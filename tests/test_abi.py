@@ -153,6 +153,30 @@ def test_f32_split_workspace_follows_shape():
     assert _abi.workspace_bytes(3, f32, 300, 260, 128) == 8192 + 50 * 16384      # 25 tiles x 2 pieces
 
 
+def test_version15_takes_any_shape_with_padded_workspace():
+    """Version 15 runs version 10 on copies of A, B and C whose rows are padded
+    to multiples of 8 halves: any shape, a workspace of version 10's own plus
+    the copies it needs (A' when K % 8, B' when N % 8 or K % 8, C' in fp32
+    when N % 8), each at a 256-byte boundary (256 CUs assumed)."""
+    from vibekernel_amd import _abi
+    from vibekernel_amd.gemm import pick_version
+    f16 = _abi.DTYPE_F16
+    up = lambda x: -(-x // 256) * 256
+    for shape in [(1000, 1001, 1000), (17, 33, 65), (4096, 4096, 4095), (1, 1, 1)]:
+        assert _abi.check(15, f16, f16, *shape, P, P, P) == 0
+        assert _abi.check(15, f16, F32, *shape, P, P, P) == 0
+    assert _abi.check(15, f16, f16, 1000, 1001, 1000, P + 8, P, P) == -4  # 16-byte aligned operands
+    m, n, k = 1000, 1001, 1000   # N off: B' and C'; version 10's plan for 1000 x 1008 x 1000 splits nothing
+    assert _abi.workspace_bytes(10, f16, m, 1008, k) == 0
+    assert _abi.workspace_bytes(15, f16, m, n, k) == up(k * 1008 * 2) + up(m * 1008 * 4)
+    m, n, k = 4096, 4096, 4095  # K off: A' and B'; C goes straight to version 10
+    assert _abi.workspace_bytes(15, f16, m, n, k) == up(m * 4096 * 2) + up(4096 * n * 2)
+    assert _abi.workspace_bytes(15, f16, 4096, 4096, 4096) == 0  # aligned: version 10 as it is
+    assert pick_version(1000, 1001, 1000) == 15 and pick_version(4096, 50257, 4096) == 15
+    assert pick_version(17, 33, 65) == 1    # below 2^24 multiply-adds: version 1, no copies
+    assert pick_version(1024, 1024, 1024) == 11
+
+
 def test_single_hip_runtime_in_process():
     """The library must bind to the HIP runtime the process already uses
     (PyTorch's), never map a second one."""
@@ -202,7 +226,7 @@ def test_pick_version_follows_shape():
     assert vk.pick_version(1, 5120, 4096) == 8     # 80 column blocks of 64 x 2 pieces: CUs idle
     assert vk.pick_version(16, 4104, 4096) == 8    # just past N = 4096
     assert vk.pick_version(16, 8224, 8192) == 8  # n % 128 != 0: the last column block cut short
-    assert vk.pick_version(16, 8220, 8192) == 1  # n % 8 != 0: the any-shape kernel
+    assert vk.pick_version(16, 8220, 8192) == 15  # n % 8 != 0: version 10 on padded copies
     assert vk.pick_version(128, 8192, 8192) == 8  # batch-128 decode: still the split-K kernel
     assert vk.pick_version(144, 8192, 8192) == 11  # from 129 rows: 128 x 128 tiles where they suit
     assert vk.pick_version(1, 8192, 8192) == 8    # one row: the same kernel, rows past M read as zeros
@@ -238,7 +262,7 @@ def test_pick_version_raises_when_no_version_accepts():
         vk.pick_version(256, 256, 256, "f32", "f16")
     assert e.value.status == -3
     with pytest.raises(vk.VkError):
-        vk.pick_version(1 << 24, 3, 8)
+        vk.pick_version(1 << 24, 3, 4096)  # A alone beyond 2^31 bytes
 
 
 def test_leave_one_out_instances_registered():

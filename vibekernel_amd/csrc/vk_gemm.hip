@@ -54,6 +54,7 @@ void init_registry() {
     register_f16_pp128();
     register_f16_skinny_sk();
     register_f16_skinny_wk();
+    register_f16_padded();
     register_f32_valu();
     register_f32_mfma();
   });
@@ -67,6 +68,12 @@ const KernelEntry* find(int version, vk_dtype in) {
 }
 
 size_t dtype_size(vk_dtype d) { return d == VK_DTYPE_F16 ? 2 : 4; }
+
+}  // namespace
+
+const KernelEntry* find_registered(int version, vk_dtype in) { return find(version, in); }
+
+namespace {
 
 struct DeviceState {
   void* ws = nullptr;

@@ -48,6 +48,10 @@ struct KernelEntry {
 
 void register_kernel(const KernelEntry& e);
 
+// The registered entry of a version (nullptr if none); for launchers that
+// run another version on a transformed problem.
+const KernelEntry* find_registered(int version, vk_dtype in);
+
 // Fill `words` 32-bit words with zero on `stream` (a kernel, not
 // hipMemsetAsync, so it may be captured into a graph).
 hipError_t zero_words(void* p, size_t words, hipStream_t stream);
@@ -60,6 +64,7 @@ void register_f16_pingpong();
 void register_f16_pp128();
 void register_f16_skinny_sk();
 void register_f16_skinny_wk();
+void register_f16_padded();
 void register_f32_valu();
 void register_f32_mfma();
 

@@ -122,7 +122,9 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
     does not suit, then the
     128 x 128 tiles of version 11 where they suit the grid, then the 256x256 kernels
     (fastest first; version 10 takes shapes off the 256 x 256 x 64 grid
-    whose N and K are multiples of 8), then the any-shape kernel.  Version 11
+    whose N and K are multiples of 8), then version 15 (version 10 through
+    row-padded copies, for N or K off the multiples of 8, from M N K = 2^24
+    on), then the any-shape kernel.  Version 11
     is taken, with T its 128 x 128 tiles on C compute units:
       * on the 256 x 256 x 64 grid, where T <= C (one wave; with 2 T <= C it
         splits K over the idle CUs itself).  Measured on MI355X, us per
@@ -185,7 +187,7 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
     convenience of the front end."""
     in_dt = DTYPE_F16 if dtype == "f16" else DTYPE_F32
     out_dt = DTYPE_F16 if (out or dtype) == "f16" else DTYPE_F32
-    order = [14, 8, 4, 11, 9, 7, 10, 6, 5, 3, 2, 1] if in_dt == DTYPE_F16 else [2, 3, 1]
+    order = [14, 8, 4, 11, 9, 7, 10, 6, 5, 3, 2, 15, 1] if in_dt == DTYPE_F16 else [2, 3, 1]
     avail = set(_abi.versions(in_dt))
 
     def takes(v):
@@ -218,6 +220,8 @@ def pick_version(m: int, n: int, k: int, dtype: str = "f16", out: str | None = N
             continue
         if v == 11 and not v11_suits():
             continue
+        if v == 15 and m * n * k < (1 << 24):
+            continue  # small shapes: version 1 without the copies
         if takes(v):
             return v
     raise VkError(-3, f"no {dtype} version accepts m={m}, n={n}, k={k} with {out or dtype} output")
