@@ -17,7 +17,11 @@
 // Each element's sum runs over the same k as version 10's on the padded
 // operands (the pad adds exact zeros), so the results are version 10's on
 // explicitly padded inputs, bit for bit.  The copies stream each operand
-// once more (at 4096 x 50257 x 4096: ~0.9 GB against ~1.7 TFLOP).
+// once more (at 4096 x 50257 x 4096: ~1.6 GB of copy traffic against ~1.7
+// TFLOP).  Measured (us per launch, one box): 4096 x 50257 x 4096 1830
+// (version 1: 33654), 4096 x 4096 x 4095 132.5 (version 10 at 4096^3:
+// 102.9), 1000 x 1001 x 1000 31.6 (version 1: 122.8); element-by-element
+// copies took 2393, 160.0 and 32.5.
 // Workspace: version 10's own (its split tails and counters, first), then
 // A', B' and C' at 256-byte boundaries.
 #include "vk_device.hpp"
@@ -61,21 +65,43 @@ PadLayout layout_of(size_t m, size_t n, size_t k, int num_cus, size_t out_bytes)
 
 // dst (drows x dpitch elements) <- src (rows x width, row pitch spitch), the
 // elements past width or rows zero.  Each thread writes 8 consecutive
-// elements of one destination row, reading the source one element at a
-// time (its rows need not be aligned); adjacent threads take adjacent
-// chunks, so every wave instruction touches contiguous bytes.
+// elements of one destination row; adjacent threads take adjacent chunks,
+// so every wave instruction touches contiguous bytes.  A chunk that lies
+// whole inside its row moves as one 16-byte access on a side whose pitch is
+// a multiple of 8 elements of 2 bytes (4 of 4 bytes: two accesses), and
+// element by element on the other side (its rows need not be aligned).
 template <typename T>
 __global__ __launch_bounds__(256) void repitch_kernel(const T* __restrict__ src, T* __restrict__ dst,
                                                       int64_t rows, int64_t width, int64_t spitch,
                                                       int64_t drows, int64_t dwidth, int64_t dpitch) {
+  constexpr int kPerVec = 16 / sizeof(T);  // elements per 16-byte access
+  const bool s_vec = spitch % kPerVec == 0, d_vec = dpitch % kPerVec == 0;
   const int64_t chunks_per_row = (dwidth + 7) / 8;
   const int64_t total = drows * chunks_per_row;
   for (int64_t c = (int64_t)blockIdx.x * 256 + threadIdx.x; c < total; c += (int64_t)gridDim.x * 256) {
     const int64_t r = c / chunks_per_row, col0 = (c - r * chunks_per_row) * 8;
+    T v[8];
+    if (r < rows && col0 + 8 <= width && s_vec) {
 #pragma unroll
-    for (int e = 0; e < 8; e++) {
-      const int64_t col = col0 + e;
-      if (col < dwidth) dst[r * dpitch + col] = (r < rows && col < width) ? src[r * spitch + col] : T(0);
+      for (int h = 0; h < 8 / kPerVec; h++) {
+        const uint4v x = *reinterpret_cast<const uint4v*>(src + r * spitch + col0 + h * kPerVec);
+        __builtin_memcpy(v + h * kPerVec, &x, 16);
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; e++) v[e] = (r < rows && col0 + e < width) ? src[r * spitch + col0 + e] : T(0);
+    }
+    if (col0 + 8 <= dwidth && d_vec) {
+#pragma unroll
+      for (int h = 0; h < 8 / kPerVec; h++) {
+        uint4v x;
+        __builtin_memcpy(&x, v + h * kPerVec, 16);
+        *reinterpret_cast<uint4v*>(dst + r * dpitch + col0 + h * kPerVec) = x;
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; e++)
+        if (col0 + e < dwidth) dst[r * dpitch + col0 + e] = v[e];
     }
   }
 }
