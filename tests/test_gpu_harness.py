@@ -31,6 +31,7 @@ RESULT_RE = re.compile(r"TFLOPS: (?P<tf>[0-9.eE+-]+); *Average Error: (?P<err>[0
     ("task1_float16_v12", (1000, 1000, 1000), 2e-4),
     ("task1_float16_v13", (768, 1024, 2048), 2e-4),
     ("task1_float16_v14", (96, 4096, 4096), 2e-4),
+    ("task1_float16_v15", (1000, 1001, 999), 2e-4),
     ("task1_float32_v1", (512, 384, 256), 1e-6),
     ("task1_float32_v2", (512, 512, 256), 1e-5),
     ("task1_float32_v3", (1000, 1000, 1000), 1e-5),
